@@ -1,0 +1,192 @@
+/*
+ * cachebridge_hip.h -- C ABI of the MI355X (gfx950) CacheBridge handoff path.
+ *
+ * The library maps source-model KV pages to target-model KV with per
+ * (target layer, target KV head) affine maps and installs the result into the
+ * target's paged KV pool:
+ *
+ *   for each target (layer l, head h) and kind in {K, V}:
+ *     X  = concat_k source[(layer, head) pair k of (l, h)]   rows of the block
+ *     K: X <- remove_rope(X, source theta)                    (fp32)
+ *     Y  = X . W[l,h] + b[l,h]                                 (W is [s*D, D] fp32)
+ *     K: Y <- apply_rope(Y, target theta)
+ *     target_pool[l][row(t)][h] = cast(Y)                      (bf16 RNE or fp32)
+ *
+ * All entry points return 0 on success or a negative errno-style code
+ * (CB_EINVAL, CB_ENOMEM, CB_EHIP) with a message from cb_last_error().
+ * Every pointer named d_* or described as "device" is a HIP device pointer;
+ * buffers are owned by the caller and must stay alive until the stream work
+ * that uses them completes. Launches are asynchronous on the given stream and
+ * never synchronize the device, except plan creation and cb_plan_read_errors.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository,
+ * cb/ = src/cachebridge/):
+ *   cb_plan_create     <- PageMapper.__init__ (cb/mapper.py:35-110): weight
+ *                         load + TP head slice, here plus MFMA pre-packing and
+ *                         resident RoPE tables (cb/rope.py:16-72).
+ *   cb_map_install     <- PageMapper.map_page (cb/mapper.py:117-239) fused with
+ *                         map_write_block / set_kv_buffer
+ *                         (cb/online/blocks.py:86-111,
+ *                         backends/sglang/runtime/r010_core.py:16-43) and the
+ *                         run-segmented install of _DirectMappedPoolCodec
+ *                         (backends/sglang/runtime/source_mapper_adapter.py:366-428).
+ *                         With an identity target index it is map_page's
+ *                         dense [2, Lt, n, Ht, D] output (cb/mapper.py:216-239).
+ *   cb_copy_rows       <- pack_source_block (cb/online/blocks.py:47-82) and the
+ *                         per-run install copies of _DirectMappedPoolCodec.copy
+ *                         (source_mapper_adapter.py:400-420).
+ */
+#ifndef CACHEBRIDGE_HIP_H
+#define CACHEBRIDGE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CB_ABI_VERSION 1
+
+#define CB_OK 0
+#define CB_EINVAL (-22)
+#define CB_ENOMEM (-12)
+#define CB_EHIP (-5)
+
+/* Element type of pages, pools and outputs. */
+#define CB_DTYPE_BF16 0
+#define CB_DTYPE_F32 1
+
+/* Job kinds. */
+#define CB_KIND_K 0
+#define CB_KIND_V 1
+
+/* How a token index t of a request maps to a row of a K/V buffer. */
+#define CB_INDEX_IDENTITY 0    /* row = t + index_offset                          */
+#define CB_INDEX_I32 1         /* row = index[t + index_offset]  (int32)          */
+#define CB_INDEX_I64 2         /* row = index[t + index_offset]  (int64)          */
+#define CB_INDEX_BLOCK_TABLE 3 /* u = t + index_offset; row = bt[u / page_size] * page_size + u % page_size (int32 bt) */
+
+/* Maximum number of window classes (e.g. sliding vs full attention layers). */
+#define CB_MAX_WINDOW_CLASSES 4
+/* Maximum support size s (source pairs per target head). */
+#define CB_MAX_SUPPORT 16
+
+/*
+ * Description of one side's K/V buffers (the source pool or page, the target
+ * pool or output). Layer l's K buffer is k_layers[l] when k_layers is not
+ * NULL (a device array of device pointers, e.g. one tensor per layer as in
+ * SGLang's MHATokenToKVPool), else k_base + l * layer_stride elements.
+ * Row r of a layer starts row_stride elements after the layer base and holds
+ * `heads` consecutive heads of head_dim elements, the first of which is head
+ * index head_offset (global source head index for sources; local target head
+ * index for targets).
+ */
+typedef struct cb_rows {
+  const void* const* k_layers;
+  const void* const* v_layers;
+  const void* k_base;
+  const void* v_base;
+  int64_t layer_stride; /* elements */
+  int64_t row_stride;   /* elements */
+  int64_t rows;         /* rows per layer; rows outside [0, rows) are skipped and flagged */
+  int32_t num_layers;   /* layers addressable through this description */
+  int32_t head_offset;
+  int32_t heads;
+  int32_t index_kind; /* CB_INDEX_* */
+  const void* index;  /* device; slot vector or block table */
+  int64_t index_offset;
+  int32_t page_size; /* CB_INDEX_BLOCK_TABLE only */
+  int32_t reserved;
+} cb_rows;
+
+/*
+ * Mapper plan description. Jobs are (target layer, target head, kind); each
+ * job has `support` source (layer, head) pairs and a [support*head_dim,
+ * head_dim] fp32 weight with y = x . W (x is the concatenation of the
+ * support rows in pair order) plus a [head_dim] fp32 bias.
+ */
+typedef struct cb_plan_desc {
+  int32_t head_dim;  /* 64 or 128 */
+  int32_t support;   /* 1..CB_MAX_SUPPORT */
+  int32_t io_dtype;  /* CB_DTYPE_* */
+  int32_t num_jobs;
+  int32_t target_layers; /* local target layers of the plan */
+  int32_t target_heads;  /* local target heads of the plan */
+  /* host arrays, one entry per job */
+  const int32_t* job_target_layer; /* [num_jobs] in [0, target_layers) */
+  const int32_t* job_target_head;  /* [num_jobs] in [0, target_heads) */
+  const int32_t* job_kind;         /* [num_jobs] CB_KIND_* */
+  const int32_t* job_window;       /* [num_jobs] window class in [0, num_windows) */
+  const int32_t* job_source_theta; /* [num_jobs] table index for un-rotation (K only) */
+  const int32_t* job_target_theta; /* [num_jobs] table index for rotation (K only) */
+  const int32_t* job_source_layer; /* [num_jobs * support] */
+  const int32_t* job_source_head;  /* [num_jobs * support] global source head */
+  /* device fp32 arrays in job order */
+  const float* d_weight; /* [num_jobs][support*head_dim][head_dim] */
+  const float* d_bias;   /* [num_jobs][head_dim] */
+  /* RoPE tables: [num_thetas][table_positions][head_dim/2] fp32 (device).
+     Entry [i][p][j] is qwen_rope(p)[j] of theta set i (the halves of the
+     reference's [tokens, head_dim] table are equal, so only one is kept). */
+  int32_t num_thetas;
+  int32_t table_positions;
+  const float* d_cos;
+  const float* d_sin;
+  /* Window classes: window_size[c] == 0 keeps every token; otherwise the
+     class keeps the last min(prefix_length, window_size[c] - 1) tokens of
+     the prefix (Gemma 3 sliding layers, cb/architectures/gemma3.py:52). */
+  int32_t num_windows;
+  int32_t window_size[CB_MAX_WINDOW_CLASSES];
+} cb_plan_desc;
+
+/* One handoff block: tokens [0, num_tokens) at positions position_start + t. */
+typedef struct cb_request {
+  cb_rows source;
+  cb_rows target;
+  int32_t num_tokens;
+  int32_t position_start;
+  int32_t prefix_length; /* whole prefix length for windows; 0 means position_start + num_tokens */
+  int32_t tokens_per_workgroup; /* 0 = library default; else a multiple of 128 */
+} cb_request;
+
+typedef struct cb_plan cb_plan;
+
+typedef struct cb_plan_info {
+  int32_t head_dim, support, io_dtype, num_jobs, target_layers, target_heads;
+  int32_t num_groups, num_thetas, table_positions, weight_terms;
+  int64_t device_bytes;
+} cb_plan_info;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* cb_last_error(void);
+int cb_abi_version(void);
+
+/* Validate, sort jobs by (window class, kind, source pairs) so that jobs
+   reading the same source rows are adjacent, pre-pack W into bf16 split
+   terms in MFMA fragment order and copy the RoPE tables. Synchronous. */
+int cb_plan_create(const cb_plan_desc* desc, cb_plan** out);
+void cb_plan_destroy(cb_plan* plan);
+int cb_plan_get_info(const cb_plan* plan, cb_plan_info* info);
+
+/* Fused gather -> un-rotate -> MFMA affine map -> bias -> rotate -> cast ->
+   scatter for every job of the plan over one request block. Asynchronous. */
+int cb_map_install(const cb_plan* plan, const cb_request* request, void* stream);
+
+/* Copy the first row_elements elements of rows of layers [0, num_layers)
+   from src to dst, K and V: dst layer l row dst_row(t) <- src layer l row
+   src_row(t) for t in [0, num_tokens). row_elements * element size must be a
+   multiple of 16 bytes. Rows outside [0, rows) are skipped and flagged in
+   *d_error_flag (bit 0 source, bit 1 target) when it is not NULL.
+   Asynchronous. */
+int cb_copy_rows(const cb_rows* src, const cb_rows* dst, int32_t num_layers,
+                 int32_t num_tokens, int32_t row_elements, int32_t dtype,
+                 int32_t* d_error_flag, void* stream);
+
+/* Read and clear the plan's device error word (bit 0: source row out of
+   range, bit 1: target row out of range). Synchronizes `stream`. */
+int cb_plan_read_errors(cb_plan* plan, int32_t* flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CACHEBRIDGE_HIP_H */

@@ -1,0 +1,188 @@
+"""GPU parity of the fused HIP handoff path against the oracle and golden vectors.
+
+Tolerance (bf16 outputs): each element within 1 bf16 ulp of the oracle, or
+within 2^-14 of its summand-magnitude bound (near-cancelling outputs, see
+``oracle/tolerance.py``); at least 99.9% within 1 ulp; normwise relative
+error <= 1e-2. fp32 outputs: within 2^-18 of the magnitude bound. Slot
+addressing and untouched rows: bit-exact.
+"""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+from safetensors.torch import load_file
+
+from cachebridge_amd import synthetic
+from cachebridge_amd.mapper import HeadwiseMapper, PageMapper
+from cachebridge_amd.online.blocks import map_install_block, map_write_block, pack_source_block
+from oracle import install as oi
+from oracle import tolerance as ot
+
+pytestmark = pytest.mark.gpu
+
+SPEC_KEYS = ("assign_layer", "assign_head", "k_weight", "v_weight", "k_bias", "v_bias")
+
+
+def _golden(golden_dir, name):
+    man = json.loads((golden_dir / "manifest.json").read_text())["files"][name + ".safetensors"]
+    return man, load_file(str(golden_dir / f"{name}.safetensors"))
+
+
+def _factor(dtype):
+    return 2.0 ** -14 if dtype == torch.bfloat16 else 2.0 ** -18
+
+
+@pytest.mark.parametrize("name", ["toy_fp32", "slice_bf16_s1", "slice_bf16_yarn"])
+def test_map_page_matches_reference_golden(golden_dir, name):
+    man, g = _golden(golden_dir, name)
+    spec = {k: g[k] for k in SPEC_KEYS}
+    yarn = man.get("yarn")
+    mapper = HeadwiseMapper.from_assignment(
+        **spec, source_rope_theta=man["source_theta"], target_rope_theta=man["target_theta"],
+        source_rope_scaling=yarn, target_rope_scaling=yarn, dtype=g["page"].dtype,
+        device="cuda", max_positions=41000)
+    page = g["page"].cuda()
+    before = page.clone()
+    out = mapper.map_page(page, position_start=man["position_start"], output_device="cuda")
+    assert torch.equal(page, before)
+    bound = ot.magnitude_bound(g["page"], spec, position_start=man["position_start"],
+                               source_theta=man["source_theta"], target_thetas=man["target_theta"],
+                               source_scaling=yarn, target_scaling=yarn)
+    stats = ot.check_mapped(out, g["out"], bound, abs_factor=_factor(g["page"].dtype))
+    print(name, stats)
+
+
+def test_reference_artifact_s8_tp_slice_matches_golden(golden_dir):
+    man, g = _golden(golden_dir, "slice_bf16_s8")
+    files = [{"selected": g["selected"], "k_weight": g["k_weight"], "k_bias": g["k_bias"],
+              "v_weight": g["v_weight"], "v_bias": g["v_bias"],
+              "headwise": torch.tensor(1, dtype=torch.int8)}]
+    mapper = PageMapper.from_tensors(files, source_rope_theta=1e4, target_rope_theta=1e6,
+                                     target_tp_rank=1, target_tp_size=2, device="cuda",
+                                     max_positions=2048)
+    output = torch.empty(2, 1, 32, 1, 128, dtype=torch.bfloat16, device="cuda")
+    result = mapper.map_page(g["page"].cuda(), position_start=1000, output_device="cuda",
+                             output=output)
+    assert result.data_ptr() == output.data_ptr()
+    compact = mapper.map_page(g["page"][:, :, :, 1:2].cuda(), position_start=1000,
+                              source_head_offset=1, output_device="cuda")
+    assert torch.equal(compact, result)
+    s = len(man["support"])
+    spec = {"assign_layer": g["selected"].view(1, 1, s), "assign_head": torch.ones(1, 1, s, dtype=torch.int64),
+            "k_weight": g["k_weight"][1:2][None], "v_weight": g["v_weight"][1:2][None],
+            "k_bias": g["k_bias"][1:2][None], "v_bias": g["v_bias"][1:2][None]}
+    bound = ot.magnitude_bound(g["page"], spec, position_start=1000, source_theta=1e4,
+                               target_thetas=1e6)
+    print(ot.check_mapped(result, g["out"], bound))
+
+
+def _cpu_pool(pool):
+    p = oi.RowStorePool(pool.layer_num, pool.size, pool.head_num, pool.head_dim, dtype=pool.dtype)
+    for l in range(pool.layer_num):
+        p.k_buffer[l].copy_(pool.k_buffer[l].cpu())
+        p.v_buffer[l].copy_(pool.v_buffer[l].cpu())
+    return p
+
+
+def _oracle_install(h, before):
+    sh = h.shape
+    tgt_slots = synthetic.slots_from_pages(h.block_table.cpu(), sh.tokens, sh.page_size)
+    mapped = oi.map_install_oracle(_cpu_pool(h.source_pool), h.source_slots.cpu().long(), before,
+                                   tgt_slots, h.spec, position_start=0,
+                                   source_theta=sh.source_theta, target_thetas=sh.target_theta,
+                                   windows=sh.windows, prefix_length=sh.tokens)
+    return mapped, tgt_slots
+
+
+def _check_pools(h, expected, mapped, tgt_slots):
+    sh = h.shape
+    written = torch.zeros(h.target_pool.size, dtype=torch.bool)
+    written[tgt_slots] = True
+    for kind, bufs, ebufs in ((0, h.target_pool.k_buffer, expected.k_buffer),
+                              (1, h.target_pool.v_buffer, expected.v_buffer)):
+        for l in range(sh.target_layers):
+            got, want = bufs[l].cpu(), ebufs[l]
+            # rows outside the request (and outside each layer's window) are untouched
+            assert torch.equal(got[~written], want[~written]), (kind, l)
+    bound_spec = {k: h.spec[k] for k in SPEC_KEYS}
+    src = h.extras["source_values"]
+    bound = ot.magnitude_bound(src, bound_spec, position_start=0, source_theta=sh.source_theta,
+                               target_thetas=sh.target_theta)
+    got = torch.stack([torch.stack([b.cpu()[tgt_slots] for b in h.target_pool.k_buffer]),
+                       torch.stack([b.cpu()[tgt_slots] for b in h.target_pool.v_buffer])])
+    first = [0 if (sh.windows is None or w is None) else max(0, sh.tokens - (w - 1))
+             for w in (sh.windows or [None] * sh.target_layers)]
+    for l in range(sh.target_layers):
+        f = first[l]
+        ot.check_mapped(got[:, l, f:], mapped[:, l, f:], bound[:, l, f:])
+        if f:
+            want_untouched = torch.stack([expected.k_buffer[l][tgt_slots[:f]],
+                                          expected.v_buffer[l][tgt_slots[:f]]])
+            assert torch.equal(got[:, l, :f], want_untouched)
+
+
+@pytest.mark.parametrize("name,tokens", [("tp4", 512), ("full", 256), ("gemma", 1200)])
+def test_fused_pool_install_matches_oracle(name, tokens):
+    sh = synthetic.shape(name, tokens=tokens)
+    if name == "gemma":
+        sh.target_layers = 12  # keeps global layers 5 and 11 and their local neighbours
+        sh.windows = sh.windows[:12]
+        sh.target_theta = sh.target_theta[:12]
+        sh.windows = [None if w is None else 1024 for w in sh.windows]
+    h = synthetic.make_handoff(sh, target_pages=128, fill_target=None)
+    torch.manual_seed(0)
+    h.target_pool.k_data.copy_(torch.randn_like(h.target_pool.k_data, dtype=torch.float32))
+    h.target_pool.v_data.copy_(torch.randn_like(h.target_pool.v_data, dtype=torch.float32))
+    before = _cpu_pool(h.target_pool)
+    h.run()
+    assert h.mapper.plan.read_errors() == 0
+    mapped, tgt_slots = _oracle_install(h, before)
+    _check_pools(h, before, mapped, tgt_slots)
+
+
+def test_blockwise_install_equals_single_launch():
+    sh = synthetic.shape("tp4", tokens=640)
+    sh.target_layers = 8
+    a = synthetic.make_handoff(sh, target_pages=80, fill_target="zeros")
+    a.run()
+    b = synthetic.make_handoff(sh, target_pages=80, fill_target="zeros")
+    for start in range(0, 640, 256):
+        b.run(start=start, stop=min(640, start + 256))
+    torch.cuda.synchronize()
+    assert torch.equal(a.target_pool.k_data, b.target_pool.k_data)
+    assert torch.equal(a.target_pool.v_data, b.target_pool.v_data)
+
+
+def test_pack_then_write_block_equals_fused_install():
+    sh = synthetic.shape("tp4", tokens=300)
+    sh.target_layers = 6
+    h = synthetic.make_handoff(sh, target_pages=64, fill_target="zeros")
+    pool = h.source_pool
+    idx64 = h.source_slots.long()
+    ws = torch.empty(2 * pool.layer_num * 512 * 2 * 128, dtype=torch.bfloat16, device="cuda")
+    block = pack_source_block(pool, idx64, start=0, stop=300, workspace=ws, block_tokens=512)
+    want = torch.stack([torch.stack([pool.k_buffer[l][idx64] for l in range(pool.layer_num)]),
+                        torch.stack([pool.v_buffer[l][idx64] for l in range(pool.layer_num)])])
+    assert torch.equal(block, want)
+    tgt_slots = synthetic.slots_from_pages(h.block_table.cpu(), 300, 16).cuda()
+    other = synthetic.make_handoff(sh, target_pages=64, fill_target="zeros")
+    map_write_block(h.mapper, block, other.target_pool, tgt_slots, start=0, source_head_offset=0)
+    h.run()
+    torch.cuda.synchronize()
+    assert torch.equal(other.target_pool.k_data, h.target_pool.k_data)
+    assert torch.equal(other.target_pool.v_data, h.target_pool.v_data)
+
+
+def test_out_of_range_slots_are_flagged_not_written():
+    sh = synthetic.shape("tp4", tokens=128)
+    sh.target_layers = 2
+    h = synthetic.make_handoff(sh, target_pages=16, fill_target="zeros")
+    bad = h.source_slots.clone()
+    bad[5] = h.source_pool.size + 7  # beyond the pool
+    map_install_block(h.mapper, h.source_pool, bad, h.target_pool, start=0, stop=128,
+                      block_table=h.block_table, page_size=16)
+    flags = h.mapper.plan.read_errors()
+    assert flags & 1
