@@ -1,0 +1,216 @@
+"""Handoff map + paged install throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload tp4]
+
+A step is one complete handoff of the workload: every target (layer, KV
+head) of the 4096-token history is mapped from its assigned source (layer,
+head) and installed into the target's paged pool through the request's block
+table (one fused kernel launch). Inputs (source pool, slots, target pool,
+block table, packed maps) are resident in HBM before the timed region.
+
+Prints one JSON line. ``value`` is mapped+installed KV tokens/s of the whole
+job; ``roofline`` prices the fused kernel's algorithmic HBM bytes (target
+writes + distinct source rows read once + fp32-equivalent maps + token index)
+per launch against MI355X HBM peak, from HIP events recorded around every
+launch on its stream; ``cpu_baseline`` times the CPU oracle on the box's host
+cores on the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "mapped+installed KV tokens/s at Qwen3-14B→32B shape; 4k-token handoff latency"
+
+WORKLOADS = {
+    "tp4": "Qwen3-14B->32B, one TP4 rank: source 40 layers x 2 KV heads -> target 64 layers x 2 "
+           "KV heads, head_dim 128, 4096 tokens, bf16, 16 of 40 source layers selected, page 16, "
+           "65536-page target pool with a shuffled free list",
+    "full": "Qwen3-14B->32B whole model on one GPU: source 40x8 -> target 64x8 KV heads, head_dim "
+            "128, 4096 tokens, bf16, page 16, 8192-page target pool",
+}
+
+
+def time_handoff(h, steps: int, warmup: int, tokens_per_workgroup: int = 0):
+    import torch
+
+    for _ in range(warmup):
+        h.run(tokens_per_workgroup=tokens_per_workgroup)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        h.run(tokens_per_workgroup=tokens_per_workgroup)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    if h.mapper.plan.read_errors() != 0:
+        raise RuntimeError("kernel flagged out-of-range rows")
+    return wall, statistics.fmean(kernel_ms), min(kernel_ms)
+
+
+def cpu_baseline(workload: str, tokens: int):
+    """CPU oracle (torch fp32, op for op as the reference mapper + row-store install)."""
+    import torch
+
+    from cachebridge_amd import synthetic
+    from oracle import install as oi
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        sh = synthetic.shape(workload, tokens=tokens)
+        spec = synthetic.mapper_spec(sh)
+        values = synthetic.source_values(sh)
+        src = oi.RowStorePool(sh.source_layers, tokens, sh.source_heads, sh.head_dim, fill=values)
+        tgt = oi.RowStorePool(sh.target_layers, tokens, sh.target_heads, sh.head_dim)
+        slots = torch.randperm(tokens, generator=torch.Generator().manual_seed(5))
+        times = []
+        for _ in range(4):
+            t0 = time.perf_counter()
+            oi.map_install_oracle(src, torch.arange(tokens), tgt, slots, spec, position_start=0,
+                                  source_theta=sh.source_theta, target_thetas=sh.target_theta)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times[1:])
+    finally:
+        torch.set_num_threads(prev)
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(tokens / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"full {workload} handoff ({tokens} tokens, all target layers and heads), "
+                      f"CPU oracle torch fp32 incl. un-RoPE of all source layers and row-store "
+                      f"install; 1 warm-up + median of 3 ({med:.2f} s each); host CPU: {cpu}"}
+
+
+def copy_calibration(mib: int = 1024, steps: int = 5) -> None:
+    """Plain row copy of ``mib`` MiB (read + write) with the library's copy kernel.
+
+    Used to scale the profiler's FETCH_SIZE / WRITE_SIZE counters: the copy
+    moves exactly ``mib`` MiB each way per launch.
+    """
+    import torch
+
+    from cachebridge_amd.plan import copy_rows, rows_from_page
+
+    rows = mib * 1024 * 1024 // (2 * 256)  # [2, 1, rows, 1, 128] bf16 = mib MiB
+    src = torch.randn(2, 1, rows, 1, 128, device="cuda").to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        copy_rows(rows_from_page(src), rows_from_page(dst), num_layers=1, num_tokens=rows,
+                  row_elements=128)
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    print(json.dumps({"copy_calibration_mib": mib, "launches": steps}), flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain MIB-MiB copy (profiler counter calibration)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="tp4", choices=sorted(WORKLOADS))
+    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--tokens-per-workgroup", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-north-star", action="store_true")
+    args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return 0
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the handoff "
+              "path runs on one GPU's share; multi-GPU sharding is not part of this build)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from cachebridge_amd import synthetic
+
+    torch.cuda.set_device(0)
+    sh = synthetic.shape(args.workload, tokens=args.tokens)
+    h = synthetic.make_handoff(sh)
+    wall, kernel_ms, kernel_min = time_handoff(h, args.steps, args.warmup, args.tokens_per_workgroup)
+    tokens = sh.tokens
+    value = args.steps * tokens / wall
+    bytes_alg = synthetic.algorithmic_bytes(sh)
+    flops = synthetic.algorithmic_flops(sh)
+    achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x per-channel lognormal(0,0.5) bf16 KV; fp32 maps "
+                "A~N(0,1/128), b~N(0,0.01))",
+        "config": {"workload": WORKLOADS[args.workload], "tokens": tokens,
+                   "target_layers": sh.target_layers, "target_kv_heads": sh.target_heads,
+                   "source_layers": sh.source_layers, "source_kv_heads": sh.source_heads,
+                   "head_dim": sh.head_dim, "page_size": sh.page_size},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "map_install_kernel<128, bf16>",
+                     "algorithmic_bytes_per_launch": bytes_alg,
+                     "kernel_ms_mean": round(kernel_ms, 5), "kernel_ms_min": round(kernel_min, 5)},
+        "mfma": {"algorithmic_tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 2),
+                 "executed_tflops": round(flops * 2.5 / (kernel_ms * 1e-3) / 1e12, 2),
+                 "peak_tflops": BF16_PEAK_TFLOPS,
+                 "executed_frac": round(flops * 2.5 / (kernel_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+        "handoff_latency_ms": round(kernel_ms, 4),
+    }
+    del h
+    torch.cuda.empty_cache()
+    if not args.no_north_star and args.workload != "full":
+        ns = synthetic.shape("full", tokens=4096)
+        hn = synthetic.make_handoff(ns)
+        wall_n, kms_n, _ = time_handoff(hn, max(20, args.steps // 4), args.warmup)
+        b = synthetic.algorithmic_bytes(ns)
+        line["north_star_64x8"] = {
+            "workload": WORKLOADS["full"], "handoff_latency_ms": round(kms_n, 4),
+            "tokens_per_s": round(ns.tokens / (kms_n * 1e-3), 1),
+            "hbm_frac": round(b / (kms_n * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_launch": b,
+        }
+        del hn
+        torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.workload, tokens)
+        line["gpu_over_cpu"] = round(value / line["cpu_baseline"]["value"], 1)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

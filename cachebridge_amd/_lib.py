@@ -133,11 +133,15 @@ class CacheBridgeHipError(RuntimeError):
 
 
 def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
-    """Load (once) and return the HIP library; raise if it is not built."""
+    """Load (once) and return the HIP library; raise if it is not built.
+
+    ``CACHEBRIDGE_HIP_LIBRARY`` names an alternative build of the same ABI.
+    """
     global _LIB
     if _LIB is not None and path is None:
         return _LIB
-    lib_path = Path(path) if path is not None else LIB_PATH
+    override = os.environ.get("CACHEBRIDGE_HIP_LIBRARY")
+    lib_path = Path(path) if path is not None else Path(override) if override else LIB_PATH
     if not lib_path.exists():
         raise RuntimeError(
             f"{lib_path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "

@@ -7,12 +7,17 @@
 //   cb/mapper.py:117-239 (map_page), cb/rope.py:9-89 (RoPE),
 //   cb/online/blocks.py:47-111 (pack_source_block, map_write_block).
 //
-// Precision: W is split on the host side of the launch (pack kernel) into
-// bf16 terms w = w0 + w1 (+ w2 for fp32 I/O); the un-rotated fp32 key is split
-// the same way in registers. Products with term-index sum below the term
-// count are accumulated in fp32 by MFMA (Henry, Tang, Heinecke, "Leveraging
-// the bfloat16 AI datatype for higher-precision computations", ARITH 2019):
-// bf16 keys 3 products, bf16 values 2 (values are bf16-exact), fp32 I/O 6.
+// Precision: W is split at plan time into bf16 terms w = w0 + w1 (+ w2 for
+// fp32 I/O); the un-rotated fp32 key is split the same way in registers.
+// Products whose term indices sum below the term count are accumulated in
+// fp32 by MFMA (Henry, Tang, Heinecke, "Leveraging the bfloat16 AI datatype
+// for higher-precision computations", ARITH 2019): bf16 keys 3 products, bf16
+// values 2 (values are bf16-exact), fp32 I/O 6.
+//
+// Un-rotation uses plan tables cos/m and sin/m with m = max(cos^2+sin^2, tiny)
+// (cb/rope.py:86-89), so the per-element IEEE divide of the reference becomes
+// a multiply; the result differs from the reference's composite rounding by at
+// most a few fp32 ulp, far below the split-bf16 contraction error.
 
 #include <hip/hip_runtime.h>
 
@@ -41,57 +46,177 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-#define CB_HIP(expr)                                                              \
-  do {                                                                            \
-    hipError_t e_ = (expr);                                                       \
+#define CB_HIP(expr)                                                                       \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
     if (e_ != hipSuccess) return fail(CB_EHIP, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Global-address-space pointers. Generic (flat) loads and stores also count
+// against the LDS wait counter, which would make every LDS wait drain all
+// outstanding HBM traffic, so every pool/table access goes through these.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define CB_GLOBAL __attribute__((address_space(1)))
+#else
+#define CB_GLOBAL
+#endif
+typedef const CB_GLOBAL char* gcptr;
+typedef CB_GLOBAL char* gptr;
+template <typename V>
+__device__ inline V gload(gcptr p) {
+  return *reinterpret_cast<const CB_GLOBAL V*>(p);
+}
+template <typename V>
+__device__ inline void gstore(gptr p, const V& v) {
+  *reinterpret_cast<CB_GLOBAL V*>(p) = v;
+}
+__device__ inline gcptr as_global(const void* p) { return (gcptr)p; }
+__device__ inline gptr as_global(void* p) { return (gptr)p; }
+__device__ inline const CB_GLOBAL float* gtab(const float* p) { return (const CB_GLOBAL float*)p; }
 
 constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
-constexpr int kColTiles = 2;                         // 16-token MFMA column tiles per wave
-constexpr int kWaveTokens = 16 * kColTiles;          // tokens per wave per sub-tile
-constexpr int kSubTokens = kWaves * kWaveTokens;     // tokens per workgroup sub-tile
 constexpr int kMaxClasses = CB_MAX_WINDOW_CLASSES;
 
-// Geometry of one (job, support) weight block for head_dim D with NTW terms.
-//   in-dim  of (k-step ks, lane group g, element e):
-//     half(ks)*D/2 + g*D/8 + (ks % (D/64))*8 + e,  half(ks) = ks / (D/64)
-//   out-dim of (row tile rt, tile row r):
-//     half(rt)*D/2 + (r/4)*D/8 + 4*(rt % (D/32)) + r%4, half(rt) = rt / (D/32)
-// so every lane group g owns dims [g*D/8, (g+1)*D/8) of both halves, which
-// puts RoPE partners j and j+D/2 in the same lane on input and output.
-template <int D, int NTW>
-struct Geo {
-  static constexpr int HALF = D / 2;
-  static constexpr int KS = D / 32;   // k-steps (MFMA K = 32)
-  static constexpr int RT = D / 16;   // output row tiles (MFMA M = 16)
-  static constexpr int G = D / 8;     // dims per lane group per half
-  static constexpr int W_U4 = RT * KS * NTW * kWave;  // uint4 per (job, support)
-};
-
-__host__ __device__ inline int in_dim(int D, int ks, int g, int e) {
-  const int per_half = D / 64;
-  return (ks / per_half) * (D / 2) + g * (D / 8) + (ks % per_half) * 8 + e;
-}
-__host__ __device__ inline int out_dim(int D, int rt, int r) {
-  const int per_half = D / 32;
-  return (rt / per_half) * (D / 2) + (r / 4) * (D / 8) + 4 * (rt % per_half) + (r % 4);
-}
+// ---------------------------------------------------------------------------
+// Element helpers
+// ---------------------------------------------------------------------------
 
 __device__ inline float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+__device__ inline float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Round-to-nearest-even fp32 -> bf16 bits; NaN -> canonical quiet NaN.
+// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ inline uint32_t pack_bf16(float a, float b) {
+  const f32x2 f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (plan-time packing).
 __device__ inline uint16_t f2bf(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
 }
+
+template <typename IO>
+struct IOTraits;
+template <>
+struct IOTraits<uint16_t> {  // bf16 storage
+  static constexpr int NTW = 2;
+  static constexpr int XT_K = 2;
+  static constexpr int XT_V = 1;
+  static constexpr int BYTES = 2;
+};
+template <>
+struct IOTraits<float> {
+  static constexpr int NTW = 3;
+  static constexpr int XT_K = 3;
+  static constexpr int XT_V = 3;
+  static constexpr int BYTES = 4;
+};
+
+// Split fp32 values into XT bf16 terms (x = t0 + t1 (+ t2) + residual); N even.
+// Term t of elements 2p, 2p+1 lands in dst[t][p] (packed bf16 pair).
+template <int XT, int N>
+__device__ inline void split_terms(const float* x, uint32_t (*dst)[N / 2]) {
+#pragma unroll
+  for (int p = 0; p < N / 2; ++p) {
+    float a = x[2 * p], b = x[2 * p + 1];
+#pragma unroll
+    for (int t = 0; t < XT; ++t) {
+      const uint32_t w = pack_bf16(a, b);
+      dst[t][p] = w;
+      a = a - lo_bf(w);
+      b = b - hi_bf(w);
+    }
+  }
+}
+
+template <int N>
+__device__ inline void load_f32(const CB_GLOBAL float* p, float* out) {
+  const CB_GLOBAL float4* q = reinterpret_cast<const CB_GLOBAL float4*>(p);
+#pragma unroll
+  for (int u = 0; u < N / 4; ++u) {
+    const float4 v = q[u];
+    out[4 * u] = v.x;
+    out[4 * u + 1] = v.y;
+    out[4 * u + 2] = v.z;
+    out[4 * u + 3] = v.w;
+  }
+}
+
+// Plan RoPE tables keep each half-row of D/2 values permuted as
+// [u][lane group g][4]: value j = g*G + 4u + e (G = D/8) sits at u*16 + g*4 + e,
+// so the four lane groups of one load instruction read 64 contiguous bytes.
+__host__ __device__ inline int tab_index(int half, int j) {
+  const int G = half / 4;
+  const int g = j / G, r = j % G;
+  return (r / 4) * 16 + g * 4 + (r % 4);
+}
+
+// Load the G table values of lane group g from one permuted half-row.
+template <int G>
+__device__ inline void load_tab(const CB_GLOBAL float* row, int g, float* out) {
+#pragma unroll
+  for (int u = 0; u < G / 4; ++u) {
+    const float4 v = *reinterpret_cast<const CB_GLOBAL float4*>(row + u * 16 + g * 4);
+    out[4 * u] = v.x;
+    out[4 * u + 1] = v.y;
+    out[4 * u + 2] = v.z;
+    out[4 * u + 3] = v.w;
+  }
+}
+
+// Unpack 16 raw bytes of IO elements to fp32 (8 bf16 or 4 fp32).
+template <typename IO>
+__device__ inline void unpack16(const uint4& v, float* out) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if constexpr (IOTraits<IO>::BYTES == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = lo_bf(w[i]);
+      out[2 * i + 1] = hi_bf(w[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(w[i]);
+  }
+}
+
+// Store N fp32 values as IO elements (N * BYTES a multiple of 8).
+template <typename IO, int N>
+__device__ inline void store_elems(gptr p, const float* v) {
+  if constexpr (IOTraits<IO>::BYTES == 2) {
+    uint32_t w[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) w[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+    if constexpr (N % 8 == 0) {
+#pragma unroll
+      for (int u = 0; u < N / 8; ++u)
+        gstore<uint4>(p + 16 * u, make_uint4(w[4 * u], w[4 * u + 1], w[4 * u + 2], w[4 * u + 3]));
+    } else {
+      static_assert(N == 4, "bf16 store width");
+      gstore<uint2>(p, make_uint2(w[0], w[1]));
+    }
+  } else {
+    static_assert(N % 4 == 0, "fp32 store width");
+#pragma unroll
+    for (int u = 0; u < N / 4; ++u)
+      gstore<float4>(p + 16 * u, make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Addressing
+// ---------------------------------------------------------------------------
 
 struct DevRows {
   const void* const* k_layers;
@@ -113,33 +238,42 @@ __device__ inline int64_t row_of(const DevRows& R, int t) {
   const int64_t u = t + R.index_offset;
   switch (R.index_kind) {
     case CB_INDEX_IDENTITY: return u;
-    case CB_INDEX_I32: return static_cast<const int32_t*>(R.index)[u];
-    case CB_INDEX_I64: return static_cast<const int64_t*>(R.index)[u];
+    case CB_INDEX_I32: return reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(R.index))[u];
+    case CB_INDEX_I64: return reinterpret_cast<const CB_GLOBAL int64_t*>(as_global(R.index))[u];
     default: {
-      const int32_t ps = R.page_size;
-      const int64_t page = static_cast<const int32_t*>(R.index)[u / ps];
-      return page * ps + u % ps;
+      const uint32_t ps = static_cast<uint32_t>(R.page_size);
+      const uint32_t uu = static_cast<uint32_t>(u);
+      const int64_t page = reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(R.index))[uu / ps];
+      return page * ps + uu % ps;
     }
   }
 }
 
-__device__ inline const char* layer_base(const DevRows& R, int kind, int layer) {
+__device__ inline gcptr layer_base(const DevRows& R, int kind, int layer) {
   const void* const* arr = kind ? R.v_layers : R.k_layers;
-  if (arr) return static_cast<const char*>(arr[layer]);
-  return (kind ? R.v_base : R.k_base) + layer * R.layer_stride_b;
+  if (arr) return as_global(*reinterpret_cast<const CB_GLOBAL void* const CB_GLOBAL*>(as_global(arr + layer)));
+  return as_global(kind ? R.v_base : R.k_base) + layer * R.layer_stride_b;
 }
+
+// ---------------------------------------------------------------------------
+// Launch arguments and work decode
+// ---------------------------------------------------------------------------
 
 struct MapArgs {
   const uint4* w;
   const float* bias;
   const int4* jobs;
   const int32_t* pairs;
-  const int32_t* group_of;
-  const int32_t* group_start;
-  const int32_t* group_size;
-  const float* cos_tab;
+  const int32_t* unit_job;      // first job of each unit (jobs of a unit are consecutive)
+  const int32_t* unit_njobs;    // jobs in each unit
+  const int32_t* unit_group;    // source group of each unit
+  const int32_t* group_unit_start;
+  const int32_t* group_unit_count;
+  const float* cos_tab;   // rotation tables [theta][pos][D/2]
   const float* sin_tab;
-  int64_t theta_stride;  // elements per theta table
+  const float* ucos_tab;  // un-rotation tables cos/m, sin/m
+  const float* usin_tab;
+  int64_t theta_stride;   // elements per theta table
   DevRows src;
   DevRows tgt;
   int32_t n_tokens;
@@ -147,7 +281,7 @@ struct MapArgs {
   int32_t support;
   int32_t chunk;
   int32_t ncls;
-  int32_t cls_job_begin[kMaxClasses];
+  int32_t cls_unit_begin[kMaxClasses];
   int32_t cls_tok_first[kMaxClasses];
   int32_t cls_tok_count[kMaxClasses];
   int32_t cls_nchunks[kMaxClasses];
@@ -155,119 +289,376 @@ struct MapArgs {
   int32_t total_items;
   int32_t padded_items;
   int32_t* err;
+  void* sink;  // scratch destination of stores without a target row
 };
 
-template <typename IO>
-struct IOTraits;
-template <>
-struct IOTraits<uint16_t> {  // bf16 storage
-  static constexpr int NTW = 2;
-  static constexpr int XT_K = 2;
-  static constexpr int XT_V = 1;
-  static constexpr int BYTES = 2;
-};
-template <>
-struct IOTraits<float> {
-  static constexpr int NTW = 3;
-  static constexpr int XT_K = 3;
-  static constexpr int XT_V = 3;
-  static constexpr int BYTES = 4;
+// Job flag (meta.z): un-rotation uses the rotation table (same theta, unit norm).
+constexpr int kJobSharedTables = 1;
+
+struct Work {
+  int job, njobs, tok_lo, tok_hi;
 };
 
-// Load n contiguous elements (n*BYTES a multiple of 16) as fp32.
-template <typename IO, int N>
-__device__ inline void load_run(const char* p, float* out) {
-  constexpr int U4 = N * IOTraits<IO>::BYTES / 16;
-  const uint4* q = reinterpret_cast<const uint4*>(p);
+// Logical item L (in XCD-aware order) -> (unit, token range). Items are
+// ordered window class, source group, chunk, unit-in-group, so units that
+// read the same source rows run back to back on one XCD and share its L2.
+__device__ inline bool decode_work(const MapArgs& a, Work* w) {
+  const int per = a.padded_items >> 3;
+  const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (L >= a.total_items) return false;
+  int c = 0;
+  while (c + 1 < a.ncls && L >= a.cls_item_begin[c + 1]) ++c;
+  const int lc = L - a.cls_item_begin[c];
+  const int nch = a.cls_nchunks[c];
+  const int ub = a.cls_unit_begin[c];
+  const int grp = a.unit_group[ub + lc / nch];
+  const int us = a.group_unit_start[grp];
+  const int un = a.group_unit_count[grp];
+  const int r = lc - (us - ub) * nch;
+  const int chunk_id = r / un;
+  const int unit = us + r % un;
+  w->job = a.unit_job[unit];
+  w->njobs = a.unit_njobs[unit];
+  w->tok_lo = a.cls_tok_first[c] + chunk_id * a.chunk;
+  w->tok_hi = min(w->tok_lo + a.chunk, a.cls_tok_first[c] + a.cls_tok_count[c]);
+  return true;
+}
+
+// MFMA product schedule: term pairs (i of x, j of w) with i + j < NTW, small first.
+template <int XT, int NTW, typename F>
+__device__ inline void for_products(F&& f) {
 #pragma unroll
-  for (int u = 0; u < U4; ++u) {
-    const uint4 v = q[u];
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    if constexpr (IOTraits<IO>::BYTES == 2) {
+  for (int lvl = NTW - 1; lvl >= 0; --lvl) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        out[u * 8 + 2 * i] = __uint_as_float(w[i] << 16);
-        out[u * 8 + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) out[u * 4 + i] = __uint_as_float(w[i]);
+    for (int i = 0; i < XT; ++i) {
+      const int j = lvl - i;
+      if (j >= 0 && j < NTW) f(i, j);
     }
   }
 }
 
-template <typename IO, int N>
-__device__ inline void store_run(char* p, const float* in) {
-  constexpr int U4 = N * IOTraits<IO>::BYTES / 16;
-  uint4* q = reinterpret_cast<uint4*>(p);
-#pragma unroll
-  for (int u = 0; u < U4; ++u) {
-    uint32_t w[4];
-    if constexpr (IOTraits<IO>::BYTES == 2) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = static_cast<uint32_t>(f2bf(in[u * 8 + 2 * i])) |
-               (static_cast<uint32_t>(f2bf(in[u * 8 + 2 * i + 1])) << 16);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(in[u * 4 + i]);
-    }
-    q[u] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
+__device__ inline f32x4 mfma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int N>
-__device__ inline void load_f32(const float* p, float* out) {
-  const float4* q = reinterpret_cast<const float4*>(p);
-#pragma unroll
-  for (int u = 0; u < N / 4; ++u) {
-    const float4 v = q[u];
-    out[4 * u] = v.x;
-    out[4 * u + 1] = v.y;
-    out[4 * u + 2] = v.z;
-    out[4 * u + 3] = v.w;
-  }
+// Input dim of (k-step ks, lane group g, element e): lane group g holds dims
+// [g*D/8, (g+1)*D/8) of both halves, k-steps walk the first half then the second.
+__host__ __device__ inline int in_dim(int D, int ks, int g, int e) {
+  const int per_half = D / 64;
+  return (ks / per_half) * (D / 2) + g * (D / 8) + (ks % per_half) * 8 + e;
 }
 
-// Split 8 fp32 values into XT bf16 terms: x = t0 + t1 (+ t2) + residual.
-template <int XT>
-__device__ inline void split8(const float* x, bf16x8* terms) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float r = x[e];
-#pragma unroll
-    for (int t = 0; t < XT; ++t) {
-      const uint16_t h = f2bf(r);
-      terms[t][e] = __builtin_bit_cast(__bf16, h);
-      r = r - bf2f(h);
-    }
-  }
+// ---------------------------------------------------------------------------
+// Streaming kernel (support s == 1)
+//
+// Workgroup = 8 waves; it owns one unit -- up to two jobs of the same kind
+// that read the same source (layer, head) -- and a contiguous token range.
+// The split-term W blocks and biases of the unit's jobs are staged in LDS once
+// (64 KB per job for D=128 bf16); then each wave independently streams
+// 16-token sub-tiles (sub-tile w, w+8, ...) with no further barriers, so the
+// waves of a CU drift apart and one wave's MFMAs overlap another's gather,
+// un-rotation and stores. Per sub-tile the source rows, RoPE table rows,
+// target slots and the un-rotated split fragments are produced once and used
+// by every job of the unit.
+//
+// Lane (col, g) holds token col of the sub-tile and input dims
+// [g*D/8, (g+1)*D/8) of both halves; output dims are permuted at pack time so
+// the lane holds the same dims of the result: RoPE partners j and j+D/2 sit
+// in one lane, and un-rotation and rotation read the same table rows.
+// ---------------------------------------------------------------------------
+
+constexpr int kUnitJobs = 2;                     // jobs per streaming unit
+constexpr int kStreamWaves = 8;
+constexpr int kStreamThreads = kWave * kStreamWaves;
+constexpr int kSubTokens = 16;                   // tokens per wave sub-tile
+constexpr int kRowSegment = 2048;                // tokens whose rows are staged in LDS at once
+constexpr int kSinkBytes = kWave * 128 * 4;       // one head row (D <= 128, fp32) per lane
+
+__host__ __device__ inline int gen_out_dim(int D, int rt, int r) {
+  const int per_half = D / 32;
+  return (rt / per_half) * (D / 2) + (r / 4) * (D / 8) + 4 * (rt % per_half) + (r % 4);
 }
 
-// Stage one (job, support) weight block into LDS; NU4 is a multiple of kThreads.
-template <int NU4>
-__device__ inline void copy_w_to_lds(uint4* lds, const uint4* __restrict__ src) {
-  constexpr int PER = NU4 / kThreads;
+// Stage NU4 uint4 into LDS with NT threads (NU4 a multiple of NT).
+template <int NU4, int NT>
+__device__ inline void copy_to_lds(uint4* lds, const uint4* __restrict__ src) {
+  constexpr int PER = NU4 / NT;
   constexpr int B = PER < 8 ? PER : 8;
-  static_assert(NU4 % kThreads == 0 && PER % B == 0, "weight block size");
-  for (int base = 0; base < NU4; base += kThreads * B) {
+  static_assert(NU4 % NT == 0 && PER % B == 0, "block size");
+  for (int base = 0; base < NU4; base += NT * B) {
     uint4 v[B];
 #pragma unroll
-    for (int i = 0; i < B; ++i) v[i] = src[base + i * kThreads + threadIdx.x];
+    for (int i = 0; i < B; ++i) v[i] = src[base + i * NT + threadIdx.x];
 #pragma unroll
-    for (int i = 0; i < B; ++i) lds[base + i * kThreads + threadIdx.x] = v[i];
+    for (int i = 0; i < B; ++i) lds[base + i * NT + threadIdx.x] = v[i];
   }
 }
 
-template <int D, typename IO, bool IS_K>
-__device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int tok_hi,
-                        int4 meta) {
-#pragma clang fp contract(off)
+template <int D, typename IO>
+struct Gm {
   using T = IOTraits<IO>;
-  using Gm = Geo<D, T::NTW>;
+  static constexpr int NTW = T::NTW;
+  static constexpr int BYTES = T::BYTES;
+  static constexpr int HALF = D / 2;
+  static constexpr int KS = D / 32;
+  static constexpr int RT = D / 16;
+  static constexpr int G = D / 8;                 // dims per lane group per half
+  static constexpr int E16 = 16 / BYTES;          // elements per 16-byte load
+  static constexpr int RUN_U4 = G / E16;          // 16-byte loads per half-run
+  static constexpr int W_U4 = RT * KS * NTW * kWave;
+};
+
+template <int D, typename IO, bool IS_K, bool SHARED, int NJ>
+__device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int32_t* lds_rows,
+                           const Work& wk) {
+  using C = Gm<D, IO>;
+  using T = IOTraits<IO>;
+  constexpr int NTW = C::NTW;
+  constexpr int XT = IS_K ? T::XT_K : T::XT_V;
+  constexpr int KS = C::KS, RT = C::RT, G = C::G, HALF = C::HALF;
+  constexpr int kind = IS_K ? CB_KIND_K : CB_KIND_V;
+  // Un-rotation table rows loaded one sub-tile ahead (keys only).
+  constexpr int TG = IS_K ? G : 1;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+
+  const int4 meta0 = a.jobs[wk.job];
+  const int sth = (meta0.y >> 16) & 0xff;
+  const int tth = (meta0.y >> 24) & 0xff;
+  const int pr = a.pairs[wk.job];
+  const int sl = pr & 0xffff;
+  const int sh = pr >> 16;
+
+  gptr tbase[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int4 m = a.jobs[wk.job + j];
+    tbase[j] = const_cast<gptr>(layer_base(a.tgt, kind, m.x & 0xffff)) +
+               static_cast<int64_t>((m.x >> 16) - a.tgt.head_offset) * D * C::BYTES;
+  }
+  // Stores of tokens without a target row go to a scratch sink, so every
+  // iteration issues a fixed number of memory operations (the compiler can
+  // then wait for the prefetched loads without also waiting for the stores).
+  gptr sink = as_global(a.sink) + lane * (D * C::BYTES);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    copy_to_lds<C::W_U4, kStreamThreads>(lds_w + j * C::W_U4, a.w + static_cast<size_t>(wk.job + j) * C::W_U4);
+    if (threadIdx.x < D) lds_bias[j * D + threadIdx.x] = a.bias[static_cast<size_t>(wk.job + j) * D + threadIdx.x];
+  }
+
+  gcptr sbase = layer_base(a.src, kind, sl) + static_cast<int64_t>(sh - a.src.head_offset) * D * C::BYTES;
+  const CB_GLOBAL float* ucos = gtab(SHARED ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* usin = gtab(SHARED ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
+  const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
+  int32_t* srows = lds_rows;
+  int32_t* trows = lds_rows + kRowSegment;
+
+  for (int seg = wk.tok_lo; seg < wk.tok_hi; seg += kRowSegment) {
+    const int seg_n = min(kRowSegment, wk.tok_hi - seg);
+    // Source and target rows of the segment's tokens (-1: skip), so that the
+    // streaming loop issues no dependent index loads.
+    __syncthreads();
+    for (int i = threadIdx.x; i < seg_n; i += kStreamThreads) {
+      const int64_t s = row_of(a.src, seg + i);
+      const int64_t d = row_of(a.tgt, seg + i);
+      const bool sok = s >= 0 && s < a.src.rows;
+      const bool dok = d >= 0 && d < a.tgt.rows;
+      if (!sok) atomicOr(a.err, 1);
+      if (!dok) atomicOr(a.err, 2);
+      srows[i] = sok ? static_cast<int32_t>(s) : -1;
+      trows[i] = dok ? static_cast<int32_t>(d) : -1;
+    }
+    __syncthreads();
+
+    const int nsub = (seg_n + kSubTokens - 1) / kSubTokens;
+    uint4 xr[2][C::RUN_U4];           // raw source dims of the next sub-tile: [half][16 B]
+    float uc[TG], us[TG];             // its un-rotation table values
+    int32_t row_next = -1;
+    auto prefetch = [&](int sub) {
+      const int i = sub * kSubTokens + col;
+      row_next = (sub < nsub && i < seg_n) ? srows[i] : -1;
+      {
+        // Rows without a source read row 0 (always valid) and are zeroed on use.
+        const int64_t r = row_next >= 0 ? row_next : 0;
+        gcptr p = sbase + r * a.src.row_stride_b + g * G * C::BYTES;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int u = 0; u < C::RUN_U4; ++u)
+            xr[h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
+      }
+      if constexpr (IS_K) {
+        const int64_t off = static_cast<int64_t>(a.position_start + seg + min(i, seg_n - 1)) * HALF;
+        load_tab<G>(ucos + off, g, uc);
+        load_tab<G>(usin + off, g, us);
+      }
+    };
+
+    int sub = wave;
+    prefetch(sub);
+    for (; sub < nsub; sub += kStreamWaves) {
+      // W fragments are re-read from LDS every sub-tile: keep the compiler from
+      // hoisting all of them into registers.
+      asm volatile("" ::: "memory");
+      const int i = sub * kSubTokens + col;
+      const int64_t trow = i < seg_n ? trows[i] : -1;
+      const bool have = row_next >= 0;
+
+      // Un-rotate (keys) and split the current sub-tile into B fragments.
+      bf16x8 bx[KS][XT];
+      float tc[SHARED ? G : 1], ts[SHARED ? G : 1];
+      {
+        float x1[G], x2[G];
+#pragma unroll
+        for (int u = 0; u < C::RUN_U4; ++u) {
+          unpack16<IO>(xr[0][u], x1 + u * C::E16);
+          unpack16<IO>(xr[1][u], x2 + u * C::E16);
+        }
+        if constexpr (IS_K) {
+#pragma unroll
+          for (int e = 0; e < G; ++e) {
+            const float k1 = x1[e] * uc[e] + x2[e] * us[e];
+            const float k2 = x2[e] * uc[e] - x1[e] * us[e];
+            x1[e] = k1;
+            x2[e] = k2;
+          }
+          if constexpr (SHARED) {
+#pragma unroll
+            for (int e = 0; e < G; ++e) {
+              tc[e] = uc[e];
+              ts[e] = us[e];
+            }
+          }
+        }
+        if (!have) {
+#pragma unroll
+          for (int e = 0; e < G; ++e) x1[e] = x2[e] = 0.f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const float* src = (ks / (KS / 2) ? x2 : x1) + (ks % (KS / 2)) * 8;
+          uint32_t tw[XT][4];
+          split_terms<XT, 8>(src, tw);
+#pragma unroll
+          for (int x = 0; x < XT; ++x)
+            bx[ks][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
+        }
+      }
+      // Next sub-tile's rows and tables load while this one is multiplied.
+      prefetch(sub + kStreamWaves);
+
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const uint4* wj = lds_w + j * C::W_U4;
+        f32x4 acc[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const float* b = lds_bias + j * D + gen_out_dim(D, rt, 4 * g);
+          acc[rt] = f32x4{b[0], b[1], b[2], b[3]};
+        }
+        // W fragments of row tile rt+1 are read from LDS while rt multiplies.
+        bf16x8 aw[2][KS][NTW];
+        auto read_w = [&](int rt, bf16x8 (&dst)[KS][NTW]) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int w = 0; w < NTW; ++w)
+              dst[ks][w] = __builtin_bit_cast(bf16x8, wj[((rt * KS + ks) * NTW + w) * kWave + lane]);
+        };
+        read_w(0, aw[0]);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          if (rt + 1 < RT) read_w(rt + 1, aw[(rt + 1) & 1]);
+          // Keep the reads above this row tile's MFMAs so they stay in flight.
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            for_products<XT, NTW>([&](int ii, int jj) { acc[rt] = mfma(aw[rt & 1][ks][jj], bx[ks][ii], acc[rt]); });
+          __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // Epilogue: target RoPE (keys), cast, scatter.
+        {
+          float o1[G], o2[G];
+#pragma unroll
+          for (int rt = 0; rt < RT / 2; ++rt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              o1[4 * rt + q] = acc[rt][q];
+              o2[4 * rt + q] = acc[rt + RT / 2][q];
+            }
+          if constexpr (IS_K) {
+            float cbuf[G], sbuf[G];
+            const float* c = tc;
+            const float* s = ts;
+            if constexpr (!SHARED) {
+              const int64_t off = static_cast<int64_t>(a.position_start + seg + i) * HALF;
+              load_tab<G>(rcos + off, g, cbuf);
+              load_tab<G>(rsin + off, g, sbuf);
+              c = cbuf;
+              s = sbuf;
+            }
+#pragma unroll
+            for (int e = 0; e < G; ++e) {
+              const float y1 = o1[e], y2 = o2[e];
+              o1[e] = y1 * c[e] - y2 * s[e];
+              o2[e] = y2 * c[e] + y1 * s[e];
+            }
+          }
+          gptr p = trow >= 0 ? tbase[j] + trow * a.tgt.row_stride_b : sink;
+          store_elems<IO, G>(p + (g * G) * C::BYTES, o1);
+          store_elems<IO, G>(p + (HALF + g * G) * C::BYTES, o2);
+        }
+      }
+    }
+  }
+}
+
+template <int D, typename IO>
+__global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapArgs a) {
+  __shared__ uint4 lds_w[kUnitJobs * Gm<D, IO>::W_U4];
+  __shared__ float lds_bias[kUnitJobs * D];
+  __shared__ int32_t lds_rows[2 * kRowSegment];
+  Work wk;
+  if (!decode_work(a, &wk)) return;
+  const int4 meta = a.jobs[wk.job];
+  const bool two = wk.njobs == 2;
+  if ((meta.y & 0xff) == CB_KIND_K) {
+    if (meta.z & kJobSharedTables) {
+      if (two) stream_run<D, IO, true, true, 2>(a, lds_w, lds_bias, lds_rows, wk);
+      else stream_run<D, IO, true, true, 1>(a, lds_w, lds_bias, lds_rows, wk);
+    } else {
+      if (two) stream_run<D, IO, true, false, 2>(a, lds_w, lds_bias, lds_rows, wk);
+      else stream_run<D, IO, true, false, 1>(a, lds_w, lds_bias, lds_rows, wk);
+    }
+  } else {
+    if (two) stream_run<D, IO, false, false, 2>(a, lds_w, lds_bias, lds_rows, wk);
+    else stream_run<D, IO, false, false, 1>(a, lds_w, lds_bias, lds_rows, wk);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// General kernel (any support s): W block of the current support staged in
+// LDS, source fragments in registers; each wave covers all output dims of 32
+// tokens. Output dims permuted so lane group g holds dims [g*D/8, (g+1)*D/8)
+// of both halves.
+// ---------------------------------------------------------------------------
+
+constexpr int kGenColTiles = 2;
+constexpr int kGenWaveTokens = 16 * kGenColTiles;
+constexpr int kGenSubTokens = kWaves * kGenWaveTokens;
+
+template <int D, typename IO, bool IS_K>
+__device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 meta) {
+  using T = IOTraits<IO>;
+  using C = Gm<D, IO>;
   constexpr int NTW = T::NTW;
   constexpr int XT = IS_K ? T::XT_K : T::XT_V;
-  constexpr int KS = Gm::KS, RT = Gm::RT, G = Gm::G, HALF = Gm::HALF;
+  constexpr int KS = C::KS, RT = C::RT, G = C::G, HALF = C::HALF;
   constexpr int kind = IS_K ? CB_KIND_K : CB_KIND_V;
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -280,54 +671,53 @@ __device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int
   const int sth = (meta.y >> 16) & 0xff;
   const int tth = (meta.y >> 24) & 0xff;
   const int S = a.support;
-  const uint4* wj = a.w + static_cast<size_t>(job) * S * Gm::W_U4;
-  const int32_t* pj = a.pairs + static_cast<size_t>(job) * S;
+  const uint4* wj = a.w + static_cast<size_t>(wk.job) * S * C::W_U4;
+  const int32_t* pj = a.pairs + static_cast<size_t>(wk.job) * S;
 
   float bias1[G], bias2[G];
-  load_f32<G>(a.bias + static_cast<size_t>(job) * D + g * G, bias1);
-  load_f32<G>(a.bias + static_cast<size_t>(job) * D + HALF + g * G, bias2);
+  load_f32<G>(gtab(a.bias) + static_cast<size_t>(wk.job) * D + g * G, bias1);
+  load_f32<G>(gtab(a.bias) + static_cast<size_t>(wk.job) * D + HALF + g * G, bias2);
 
-  char* tbase = const_cast<char*>(layer_base(a.tgt, kind, tl)) +
+  gptr tbase = const_cast<gptr>(layer_base(a.tgt, kind, tl)) +
                 static_cast<int64_t>(th - a.tgt.head_offset) * D * T::BYTES;
-  const float* cos_s = a.cos_tab + sth * a.theta_stride;
-  const float* sin_s = a.sin_tab + sth * a.theta_stride;
-  const float* cos_t = a.cos_tab + tth * a.theta_stride;
-  const float* sin_t = a.sin_tab + tth * a.theta_stride;
+  const CB_GLOBAL float* ucos = gtab(a.ucos_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* usin = gtab(a.usin_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
+  const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
 
   if (S == 1) {
-    copy_w_to_lds<Gm::W_U4>(lds_w, wj);
+    copy_to_lds<C::W_U4, kThreads>(lds_w, wj);
     __syncthreads();
   }
 
-  for (int sub = tok_lo; sub < tok_hi; sub += kSubTokens) {
-    int tok[kColTiles];
-    bool valid[kColTiles];
+  for (int sub = wk.tok_lo; sub < wk.tok_hi; sub += kGenSubTokens) {
+    int tok[kGenColTiles];
+    bool valid[kGenColTiles];
 #pragma unroll
-    for (int ct = 0; ct < kColTiles; ++ct) {
-      tok[ct] = sub + wave * kWaveTokens + ct * 16 + col;
-      valid[ct] = tok[ct] < tok_hi;
+    for (int ct = 0; ct < kGenColTiles; ++ct) {
+      tok[ct] = sub + wave * kGenWaveTokens + ct * 16 + col;
+      valid[ct] = tok[ct] < wk.tok_hi;
     }
-    f32x4 acc[RT][kColTiles];
+    f32x4 acc[RT][kGenColTiles];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < kColTiles; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ct = 0; ct < kGenColTiles; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int k = 0; k < S; ++k) {
       if (S > 1) {
         __syncthreads();
-        copy_w_to_lds<Gm::W_U4>(lds_w, wj + static_cast<size_t>(k) * Gm::W_U4);
+        copy_to_lds<C::W_U4, kThreads>(lds_w, wj + static_cast<size_t>(k) * C::W_U4);
         __syncthreads();
       }
       const int pr = pj[k];
       const int sl = pr & 0xffff;
       const int sh = pr >> 16;
-      const char* sbase = layer_base(a.src, kind, sl) +
-                          static_cast<int64_t>(sh - a.src.head_offset) * D * T::BYTES;
+      gcptr sbase = layer_base(a.src, kind, sl) + static_cast<int64_t>(sh - a.src.head_offset) * D * T::BYTES;
 
-      bf16x8 bx[KS][kColTiles][XT];
+      bf16x8 bx[KS][kGenColTiles][XT];
 #pragma unroll
-      for (int ct = 0; ct < kColTiles; ++ct) {
+      for (int ct = 0; ct < kGenColTiles; ++ct) {
         float x1[G], x2[G];
         bool ok = valid[ct];
         int64_t row = 0;
@@ -339,22 +729,23 @@ __device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int
           }
         }
         if (ok) {
-          const char* p = sbase + row * a.src.row_stride_b;
-          load_run<IO, G>(p + (g * G) * T::BYTES, x1);
-          load_run<IO, G>(p + (HALF + g * G) * T::BYTES, x2);
+          gcptr p = sbase + row * a.src.row_stride_b;
+#pragma unroll
+          for (int u = 0; u < G / C::E16; ++u) {
+            unpack16<IO>(gload<uint4>(p + (g * G + u * C::E16) * T::BYTES), x1 + u * C::E16);
+            unpack16<IO>(gload<uint4>(p + (HALF + g * G + u * C::E16) * T::BYTES), x2 + u * C::E16);
+          }
           if constexpr (IS_K) {
-            // remove_rope: (x*cos - rotate_half(x)*sin) / max(cos^2 + sin^2, tiny)
-            const int pos = a.position_start + tok[ct];
+            const int64_t off = static_cast<int64_t>(a.position_start + tok[ct]) * HALF;
             float c[G], s[G];
-            load_f32<G>(cos_s + static_cast<int64_t>(pos) * HALF + g * G, c);
-            load_f32<G>(sin_s + static_cast<int64_t>(pos) * HALF + g * G, s);
+            load_tab<G>(ucos + off, g, c);
+            load_tab<G>(usin + off, g, s);
 #pragma unroll
             for (int e = 0; e < G; ++e) {
-              const float m = fmaxf(c[e] * c[e] + s[e] * s[e], 1.17549435e-38f);
-              const float a1 = (x1[e] * c[e] + x2[e] * s[e]) / m;
-              const float a2 = (x2[e] * c[e] - x1[e] * s[e]) / m;
-              x1[e] = a1;
-              x2[e] = a2;
+              const float k1 = x1[e] * c[e] + x2[e] * s[e];
+              const float k2 = x2[e] * c[e] - x1[e] * s[e];
+              x1[e] = k1;
+              x2[e] = k2;
             }
           }
         } else {
@@ -363,9 +754,12 @@ __device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const int half_idx = ks / (KS / 2);
-          const int sub8 = ks % (KS / 2);
-          split8<XT>((half_idx ? x2 : x1) + sub8 * 8, bx[ks][ct]);
+          const float* src = (ks / (KS / 2) ? x2 : x1) + (ks % (KS / 2)) * 8;
+          uint32_t tw[XT][4];
+          split_terms<XT, 8>(src, tw);
+#pragma unroll
+          for (int x = 0; x < XT; ++x)
+            bx[ks][ct][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
         }
       }
 
@@ -378,26 +772,14 @@ __device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int
           for (int t = 0; t < NTW; ++t)
             aw[t] = __builtin_bit_cast(bf16x8, lds_w[((rt * KS + ks) * NTW + t) * kWave + lane]);
 #pragma unroll
-          for (int ct = 0; ct < kColTiles; ++ct) {
-            // small terms first: sum of term indices from NTW-1 down to 0
-#pragma unroll
-            for (int lvl = NTW - 1; lvl >= 0; --lvl) {
-#pragma unroll
-              for (int i = 0; i < XT; ++i) {
-                const int j = lvl - i;
-                if (j < 0 || j >= NTW) continue;
-                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aw[j], bx[ks][ct][i],
-                                                                      acc[rt][ct], 0, 0, 0);
-              }
-            }
-          }
+          for (int ct = 0; ct < kGenColTiles; ++ct)
+            for_products<XT, NTW>([&](int i, int j) { acc[rt][ct] = mfma(aw[j], bx[ks][ct][i], acc[rt][ct]); });
         }
       }
     }
 
-    // Epilogue: bias, target RoPE (keys), cast, scatter through the target index.
 #pragma unroll
-    for (int ct = 0; ct < kColTiles; ++ct) {
+    for (int ct = 0; ct < kGenColTiles; ++ct) {
       if (!valid[ct]) continue;
       const int64_t row = row_of(a.tgt, tok[ct]);
       if (row < 0 || row >= a.tgt.rows) {
@@ -407,9 +789,9 @@ __device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int
       float o1[G], o2[G];
       float c[G], s[G];
       if constexpr (IS_K) {
-        const int pos = a.position_start + tok[ct];
-        load_f32<G>(cos_t + static_cast<int64_t>(pos) * HALF + g * G, c);
-        load_f32<G>(sin_t + static_cast<int64_t>(pos) * HALF + g * G, s);
+        const int64_t off = static_cast<int64_t>(a.position_start + tok[ct]) * HALF;
+        load_tab<G>(rcos + off, g, c);
+        load_tab<G>(rsin + off, g, s);
       }
 #pragma unroll
       for (int rt = 0; rt < RT / 2; ++rt) {
@@ -419,7 +801,6 @@ __device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int
           const float y1 = acc[rt][ct][i] + bias1[e];
           const float y2 = acc[rt + RT / 2][ct][i] + bias2[e];
           if constexpr (IS_K) {
-            // apply_rope: x*cos + rotate_half(x)*sin
             o1[e] = y1 * c[e] - y2 * s[e];
             o2[e] = y2 * c[e] + y1 * s[e];
           } else {
@@ -428,40 +809,28 @@ __device__ void run_job(const MapArgs& a, uint4* lds_w, int job, int tok_lo, int
           }
         }
       }
-      char* p = tbase + row * a.tgt.row_stride_b;
-      store_run<IO, G>(p + (g * G) * T::BYTES, o1);
-      store_run<IO, G>(p + (HALF + g * G) * T::BYTES, o2);
+      gptr p = tbase + row * a.tgt.row_stride_b;
+      store_elems<IO, G>(p + (g * G) * T::BYTES, o1);
+      store_elems<IO, G>(p + (HALF + g * G) * T::BYTES, o2);
     }
   }
 }
 
 template <int D, typename IO>
-__global__ __launch_bounds__(kThreads) void map_install_kernel(MapArgs a) {
-  __shared__ uint4 lds_w[Geo<D, IOTraits<IO>::NTW>::W_U4];
-  // XCD-aware order: consecutive logical items land on the same XCD, so jobs
-  // that share source rows (adjacent after plan sorting) share that L2.
-  const int per = a.padded_items >> 3;
-  const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-  if (L >= a.total_items) return;
-  int c = 0;
-  while (c + 1 < a.ncls && L >= a.cls_item_begin[c + 1]) ++c;
-  const int lc = L - a.cls_item_begin[c];
-  const int nch = a.cls_nchunks[c];
-  const int jb = a.cls_job_begin[c];
-  const int grp = a.group_of[jb + lc / nch];
-  const int gs = a.group_start[grp];
-  const int gn = a.group_size[grp];
-  const int r = lc - (gs - jb) * nch;
-  const int chunk_id = r / gn;
-  const int job = gs + r % gn;
-  const int tok_lo = a.cls_tok_first[c] + chunk_id * a.chunk;
-  const int tok_hi = min(tok_lo + a.chunk, a.cls_tok_first[c] + a.cls_tok_count[c]);
-  const int4 meta = a.jobs[job];
+__global__ __launch_bounds__(kThreads) void map_install_gen_kernel(MapArgs a) {
+  __shared__ uint4 lds_w[Gm<D, IO>::W_U4];
+  Work wk;
+  if (!decode_work(a, &wk)) return;
+  const int4 meta = a.jobs[wk.job];
   if ((meta.y & 0xff) == CB_KIND_K)
-    run_job<D, IO, true>(a, lds_w, job, tok_lo, tok_hi, meta);
+    gen_run<D, IO, true>(a, lds_w, wk, meta);
   else
-    run_job<D, IO, false>(a, lds_w, job, tok_lo, tok_hi, meta);
+    gen_run<D, IO, false>(a, lds_w, wk, meta);
 }
+
+// ---------------------------------------------------------------------------
+// Plan-time kernels
+// ---------------------------------------------------------------------------
 
 // Pack fp32 W[orig][s*D][D] into bf16 split terms in MFMA A-fragment order,
 // and permute the bias to sorted job order.
@@ -469,8 +838,8 @@ template <int D, int NTW>
 __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __restrict__ bias,
                                     const int32_t* __restrict__ order, int njobs, int S,
                                     uint16_t* __restrict__ wp, float* __restrict__ bp) {
-  using Gm = Geo<D, NTW>;
-  const int64_t per_block = static_cast<int64_t>(Gm::W_U4) * 8;  // bf16 per (job, support)
+  constexpr int KS = D / 32, RT = D / 16;
+  const int64_t per_block = static_cast<int64_t>(RT) * KS * NTW * kWave * 8;
   const int64_t total = per_block * S * njobs;
   for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
        idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -478,13 +847,13 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
     const int e = rem % 8; rem /= 8;
     const int lane = rem % kWave; rem /= kWave;
     const int t = rem % NTW; rem /= NTW;
-    const int ks = rem % Gm::KS; rem /= Gm::KS;
-    const int rt = rem % Gm::RT; rem /= Gm::RT;
+    const int ks = rem % KS; rem /= KS;
+    const int rt = rem % RT; rem /= RT;
+    const int fo = gen_out_dim(D, rt, lane & 15);
     const int k = rem % S; rem /= S;
     const int j = static_cast<int>(rem);
     const int src_job = order[j];
     const int fi = k * D + in_dim(D, ks, lane >> 4, e);
-    const int fo = out_dim(D, rt, lane & 15);
     float r = w[(static_cast<int64_t>(src_job) * S * D + fi) * D + fo];
     uint16_t h = 0;
     for (int tt = 0; tt <= t; ++tt) {
@@ -501,7 +870,32 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
   }
 }
 
+// Plan tables from standard [theta][pos][D/2] cos/sin: rotation tables and
+// un-rotation tables cos/m, sin/m (m = max(cos^2 + sin^2, FLT_MIN)), both in
+// the permuted half-row layout; also max |m - 1| per theta set (as float bits).
+__global__ void prepare_tables_kernel(const float* __restrict__ c, const float* __restrict__ s,
+                                      float* __restrict__ rc, float* __restrict__ rs,
+                                      float* __restrict__ uc, float* __restrict__ us, int64_t n,
+                                      int half, int64_t per_theta, unsigned* __restrict__ norm_dev) {
+#pragma clang fp contract(off)
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float cc = c[i], ss = s[i];
+    const float m = fmaxf(cc * cc + ss * ss, 1.17549435e-38f);
+    const int64_t row = i / half;
+    const int64_t o = row * half + tab_index(half, static_cast<int>(i % half));
+    rc[o] = cc;
+    rs[o] = ss;
+    uc[o] = cc / m;
+    us[o] = ss / m;
+    atomicMax(norm_dev + i / per_theta, __float_as_uint(fabsf(m - 1.0f)));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Row copy: dst layer l row(t) <- src layer l row(t), 16-byte chunks.
+// ---------------------------------------------------------------------------
+
 struct CopyArgs {
   DevRows src, dst;
   int32_t num_tokens;
@@ -515,8 +909,8 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(CopyArgs a) {
   const int lk = blockIdx.x / a.blocks_per_layer;  // layer * 2 + kind
   const int tb = blockIdx.x % a.blocks_per_layer;
   const int layer = lk >> 1, kind = lk & 1;
-  const char* sbase = layer_base(a.src, kind, layer);
-  char* dbase = const_cast<char*>(layer_base(a.dst, kind, layer));
+  gcptr sbase = layer_base(a.src, kind, layer);
+  gptr dbase = const_cast<gptr>(layer_base(a.dst, kind, layer));
   const int t0 = tb * a.tokens_per_block;
   const int n = min(a.tokens_per_block, a.num_tokens - t0);
   const int cpr = a.chunks_per_row;
@@ -533,12 +927,16 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(CopyArgs a) {
       if (a.err && ch == 0) atomicOr(a.err, 2);
       continue;
     }
-    const uint4 v = reinterpret_cast<const uint4*>(sbase + sr * a.src.row_stride_b)[ch];
-    reinterpret_cast<uint4*>(dbase + dr * a.dst.row_stride_b)[ch] = v;
+    const uint4 v = gload<uint4>(sbase + sr * a.src.row_stride_b + 16 * ch);
+    gstore<uint4>(dbase + dr * a.dst.row_stride_b + 16 * ch, v);
   }
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
 
 struct cb_plan {
   int device = 0;
@@ -547,28 +945,35 @@ struct cb_plan {
   int elem_bytes = 2;
   int num_windows = 1;
   int window_size[kMaxClasses] = {0, 0, 0, 0};
-  int cls_job_begin[kMaxClasses] = {0, 0, 0, 0};
-  int cls_job_end[kMaxClasses] = {0, 0, 0, 0};
+  int cls_unit_begin[kMaxClasses] = {0, 0, 0, 0};
+  int cls_unit_end[kMaxClasses] = {0, 0, 0, 0};
   int max_src_layer = 0, min_src_head = 0, max_src_head = 0;
   int max_tgt_layer = 0, min_tgt_head = 0, max_tgt_head = 0;
   void* d_w = nullptr;
   float* d_bias = nullptr;
   int4* d_jobs = nullptr;
   int32_t* d_pairs = nullptr;
-  int32_t* d_group_of = nullptr;
-  int32_t* d_group_start = nullptr;
-  int32_t* d_group_size = nullptr;
+  int32_t* d_unit_job = nullptr;
+  int32_t* d_unit_njobs = nullptr;
+  int32_t* d_unit_group = nullptr;
+  int32_t* d_group_unit_start = nullptr;
+  int32_t* d_group_unit_count = nullptr;
   float* d_cos = nullptr;
   float* d_sin = nullptr;
+  float* d_ucos = nullptr;
+  float* d_usin = nullptr;
   int32_t* d_err = nullptr;
+  void* d_sink = nullptr;
 };
 
 namespace {
 
 void plan_free(cb_plan* p) {
   if (!p) return;
-  void* ptrs[] = {p->d_w, p->d_bias, p->d_jobs, p->d_pairs, p->d_group_of, p->d_group_start,
-                  p->d_group_size, p->d_cos, p->d_sin, p->d_err};
+  void* ptrs[] = {p->d_w,         p->d_bias,         p->d_jobs,           p->d_pairs,
+                  p->d_unit_job,  p->d_unit_njobs,   p->d_unit_group,     p->d_group_unit_start,
+                  p->d_group_unit_count, p->d_cos,   p->d_sin,            p->d_ucos,
+                  p->d_usin,      p->d_err,          p->d_sink};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
   delete p;
@@ -602,7 +1007,8 @@ int to_dev_rows(const cb_rows& r, int elem_bytes, DevRows* out) {
     return fail(CB_EINVAL, "index pointer required for index_kind %d", r.index_kind);
   if (r.index_kind == CB_INDEX_BLOCK_TABLE && r.page_size <= 0)
     return fail(CB_EINVAL, "block table needs page_size > 0");
-  if (r.index_offset < 0) return fail(CB_EINVAL, "index_offset must be >= 0");
+  if (r.index_offset < 0 || r.index_offset > (int64_t{1} << 30))
+    return fail(CB_EINVAL, "index_offset out of range");
   if (r.rows <= 0) return fail(CB_EINVAL, "rows must be > 0");
   if (!r.k_layers && (!r.k_base || !r.v_base))
     return fail(CB_EINVAL, "either per-layer pointer arrays or k_base/v_base are required");
@@ -614,6 +1020,11 @@ int to_dev_rows(const cb_rows& r, int elem_bytes, DevRows* out) {
   return CB_OK;
 }
 
+template <int D, int NTW>
+void launch_pack(const cb_plan_desc* d, const int32_t* d_order, uint16_t* wp, float* bp) {
+  hipLaunchKernelGGL((pack_weights_kernel<D, NTW>), dim3(1024), dim3(256), 0, 0, d->d_weight, d->d_bias,
+                     d_order, d->num_jobs, d->support, wp, bp);
+}
 
 template <typename SameGroup>
 int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup same_group,
@@ -626,22 +1037,25 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   p->num_windows = d->num_windows;
   for (int c = 0; c < kMaxClasses; ++c) {
     p->window_size[c] = c < d->num_windows ? d->window_size[c] : 0;
-    p->cls_job_begin[c] = p->cls_job_end[c] = c < d->num_windows ? -1 : 0;
+    p->cls_unit_begin[c] = p->cls_unit_end[c] = c < d->num_windows ? -1 : 0;
   }
   std::vector<int4> jobs(nj);
-  std::vector<int32_t> pairs(static_cast<size_t>(nj) * S), group_of(nj);
-  std::vector<int32_t> gstart, gsize;
+  std::vector<int32_t> pairs(static_cast<size_t>(nj) * S);
+  std::vector<int32_t> unit_job, unit_njobs, unit_group, group_unit_start, group_unit_count;
   p->max_src_layer = 0;
   p->min_src_head = 1 << 30;
   p->max_src_head = 0;
   p->max_tgt_layer = 0;
   p->min_tgt_head = 1 << 30;
   p->max_tgt_head = 0;
+  // Units: runs of up to kUnitJobs consecutive jobs of one group for the
+  // streaming kernel (s == 1); single jobs for the general kernel.
+  const int unit_cap = S == 1 ? kUnitJobs : 1;
   for (int i = 0; i < nj; ++i) {
     const int j = order[i];
     jobs[i] = make_int4(d->job_target_layer[j] | (d->job_target_head[j] << 16),
-                        d->job_kind[j] | (d->job_window[j] << 8) |
-                            (d->job_source_theta[j] << 16) | (d->job_target_theta[j] << 24),
+                        d->job_kind[j] | (d->job_window[j] << 8) | (d->job_source_theta[j] << 16) |
+                            (d->job_target_theta[j] << 24),
                         0, j);
     for (int k = 0; k < S; ++k) {
       const int sl = d->job_source_layer[j * S + k], sh = d->job_source_head[j * S + k];
@@ -653,50 +1067,79 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     p->max_tgt_layer = std::max(p->max_tgt_layer, d->job_target_layer[j]);
     p->min_tgt_head = std::min(p->min_tgt_head, d->job_target_head[j]);
     p->max_tgt_head = std::max(p->max_tgt_head, d->job_target_head[j]);
-    if (i == 0 || !same_group(order[i - 1], j)) {
-      gstart.push_back(i);
-      gsize.push_back(0);
+    const bool new_group = i == 0 || !same_group(order[i - 1], j);
+    if (new_group) {
+      group_unit_start.push_back(static_cast<int32_t>(unit_job.size()));
+      group_unit_count.push_back(0);
     }
-    gsize.back() += 1;
-    group_of[i] = static_cast<int32_t>(gstart.size() - 1);
-    const int c = d->job_window[j];
-    if (p->cls_job_begin[c] < 0) p->cls_job_begin[c] = i;
-    p->cls_job_end[c] = i + 1;
+    if (new_group || unit_njobs.back() == unit_cap) {
+      unit_job.push_back(i);
+      unit_njobs.push_back(0);
+      unit_group.push_back(static_cast<int32_t>(group_unit_start.size() - 1));
+      group_unit_count.back() += 1;
+      const int c = d->job_window[j];
+      const int u = static_cast<int>(unit_job.size() - 1);
+      if (p->cls_unit_begin[c] < 0) p->cls_unit_begin[c] = u;
+      p->cls_unit_end[c] = u + 1;
+    }
+    unit_njobs.back() += 1;
   }
   for (int c = 0; c < d->num_windows; ++c)
-    if (p->cls_job_begin[c] < 0) p->cls_job_begin[c] = p->cls_job_end[c] = 0;
+    if (p->cls_unit_begin[c] < 0) p->cls_unit_begin[c] = p->cls_unit_end[c] = 0;
 
   const size_t w_elems = static_cast<size_t>(nj) * S * (D / 16) * (D / 32) * p->ntw * kWave * 8;
   const size_t table = static_cast<size_t>(d->num_thetas) * d->table_positions * (D / 2);
   int rc;
-  if ((rc = upload(&p->d_jobs, jobs.data(), jobs.size() * sizeof(int4), &bytes))) return rc;
   if ((rc = upload(&p->d_pairs, pairs.data(), pairs.size() * 4, &bytes))) return rc;
-  if ((rc = upload(&p->d_group_of, group_of.data(), group_of.size() * 4, &bytes))) return rc;
-  if ((rc = upload(&p->d_group_start, gstart.data(), gstart.size() * 4, &bytes))) return rc;
-  if ((rc = upload(&p->d_group_size, gsize.data(), gsize.size() * 4, &bytes))) return rc;
+  if ((rc = upload(&p->d_unit_job, unit_job.data(), unit_job.size() * 4, &bytes))) return rc;
+  if ((rc = upload(&p->d_unit_njobs, unit_njobs.data(), unit_njobs.size() * 4, &bytes))) return rc;
+  if ((rc = upload(&p->d_unit_group, unit_group.data(), unit_group.size() * 4, &bytes))) return rc;
+  if ((rc = upload(&p->d_group_unit_start, group_unit_start.data(), group_unit_start.size() * 4, &bytes))) return rc;
+  if ((rc = upload(&p->d_group_unit_count, group_unit_count.data(), group_unit_count.size() * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_w, nullptr, w_elems * 2, &bytes))) return rc;
   if ((rc = upload(&p->d_bias, nullptr, static_cast<size_t>(nj) * D * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_cos, nullptr, table * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_sin, nullptr, table * 4, &bytes))) return rc;
+  if ((rc = upload(&p->d_ucos, nullptr, table * 4, &bytes))) return rc;
+  if ((rc = upload(&p->d_usin, nullptr, table * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_err, nullptr, 4, &bytes))) return rc;
-  CB_HIP(hipMemcpy(p->d_cos, d->d_cos, table * 4, hipMemcpyDeviceToDevice));
-  CB_HIP(hipMemcpy(p->d_sin, d->d_sin, table * 4, hipMemcpyDeviceToDevice));
+  if ((rc = upload(&p->d_sink, nullptr, kSinkBytes, &bytes))) return rc;
   CB_HIP(hipMemset(p->d_err, 0, 4));
+  // Rotation / un-rotation tables in the permuted layout, and which theta sets
+  // have unit norm (|cos^2 + sin^2 - 1| <= 2 ulp) so keys can share one table.
+  {
+    unsigned* d_norm = nullptr;
+    CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_norm), d->num_thetas * sizeof(unsigned)));
+    std::vector<unsigned> norm(d->num_thetas, 0u);
+    hipError_t e = hipMemset(d_norm, 0, d->num_thetas * sizeof(unsigned));
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(prepare_tables_kernel, dim3(1024), dim3(256), 0, 0, d->d_cos, d->d_sin,
+                         p->d_cos, p->d_sin, p->d_ucos, p->d_usin, static_cast<int64_t>(table), D / 2,
+                         static_cast<int64_t>(d->table_positions) * (D / 2), d_norm);
+      e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(norm.data(), d_norm, norm.size() * sizeof(unsigned), hipMemcpyDeviceToHost);
+    (void)hipFree(d_norm);
+    if (e != hipSuccess) return fail(CB_EHIP, "plan table preparation failed: %s", hipGetErrorString(e));
+    for (int i = 0; i < nj; ++i) {
+      const int sth = (jobs[i].y >> 16) & 0xff, tth = (jobs[i].y >> 24) & 0xff;
+      float dev;
+      std::memcpy(&dev, &norm[sth], sizeof(dev));
+      if (sth == tth && dev <= 2.4e-7f) jobs[i].z |= kJobSharedTables;
+    }
+    if ((rc = upload(&p->d_jobs, jobs.data(), jobs.size() * sizeof(int4), &bytes))) return rc;
+  }
   int32_t* d_order = nullptr;
   CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), order.size() * 4));
   hipError_t e = hipMemcpy(d_order, order.data(), order.size() * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    const dim3 grid(1024), block(256);
     uint16_t* wp = static_cast<uint16_t*>(p->d_w);
     if (D == 64 && p->ntw == 2)
-      hipLaunchKernelGGL((pack_weights_kernel<64, 2>), grid, block, 0, 0, d->d_weight, d->d_bias,
-                         d_order, nj, S, wp, p->d_bias);
+      launch_pack<64, 2>(d, d_order, wp, p->d_bias);
     else if (D == 64)
-      hipLaunchKernelGGL((pack_weights_kernel<64, 3>), grid, block, 0, 0, d->d_weight, d->d_bias,
-                         d_order, nj, S, wp, p->d_bias);
+      launch_pack<64, 3>(d, d_order, wp, p->d_bias);
     else
-      hipLaunchKernelGGL((pack_weights_kernel<128, 2>), grid, block, 0, 0, d->d_weight, d->d_bias,
-                         d_order, nj, S, wp, p->d_bias);
+      launch_pack<128, 2>(d, d_order, wp, p->d_bias);
     e = hipGetLastError();
   }
   if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -708,12 +1151,24 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   p->info.num_jobs = nj;
   p->info.target_layers = d->target_layers;
   p->info.target_heads = d->target_heads;
-  p->info.num_groups = static_cast<int32_t>(gstart.size());
+  p->info.num_groups = static_cast<int32_t>(group_unit_start.size());
   p->info.num_thetas = d->num_thetas;
   p->info.table_positions = d->table_positions;
   p->info.weight_terms = p->ntw;
   p->info.device_bytes = bytes;
   return CB_OK;
+}
+
+// Default tokens per workgroup: about three workgroups per CU over the launch
+// (one resident per CU for the streaming kernel), at least 512 tokens.
+int default_chunk(const cb_plan* p, int n) {
+  if (p->info.support != 1) return kGenSubTokens;
+  int64_t units = 0;
+  for (int c = 0; c < p->num_windows; ++c) units += p->cls_unit_end[c] - p->cls_unit_begin[c];
+  const int64_t target_items = 768;
+  int64_t chunk = (units * n + target_items - 1) / target_items;
+  chunk = std::max<int64_t>(512, (chunk + kSubTokens - 1) / kSubTokens * kSubTokens);
+  return static_cast<int>(std::min<int64_t>(chunk, 1 << 20));
 }
 
 }  // namespace
@@ -774,12 +1229,18 @@ int cb_plan_create(const cb_plan_desc* d, cb_plan** out) {
     }
   }
 
-  // Sort jobs: window class, kind, source pairs, then target position.
+  // Sort jobs: window class, kind, RoPE theta sets, source pairs, then target
+  // position. A group (same class, kind, thetas and source pairs) reads the
+  // same source rows and tables.
   std::vector<int> order(nj);
   std::iota(order.begin(), order.end(), 0);
   auto key_less = [&](int x, int y) {
     if (d->job_window[x] != d->job_window[y]) return d->job_window[x] < d->job_window[y];
     if (d->job_kind[x] != d->job_kind[y]) return d->job_kind[x] < d->job_kind[y];
+    if (d->job_source_theta[x] != d->job_source_theta[y])
+      return d->job_source_theta[x] < d->job_source_theta[y];
+    if (d->job_target_theta[x] != d->job_target_theta[y])
+      return d->job_target_theta[x] < d->job_target_theta[y];
     for (int k = 0; k < S; ++k) {
       const int a0 = d->job_source_layer[x * S + k], b0 = d->job_source_layer[y * S + k];
       if (a0 != b0) return a0 < b0;
@@ -792,7 +1253,10 @@ int cb_plan_create(const cb_plan_desc* d, cb_plan** out) {
   };
   std::stable_sort(order.begin(), order.end(), key_less);
   auto same_group = [&](int x, int y) {
-    if (d->job_window[x] != d->job_window[y] || d->job_kind[x] != d->job_kind[y]) return false;
+    if (d->job_window[x] != d->job_window[y] || d->job_kind[x] != d->job_kind[y] ||
+        d->job_source_theta[x] != d->job_source_theta[y] ||
+        d->job_target_theta[x] != d->job_target_theta[y])
+      return false;
     for (int k = 0; k < S; ++k)
       if (d->job_source_layer[x * S + k] != d->job_source_layer[y * S + k] ||
           d->job_source_head[x * S + k] != d->job_source_head[y * S + k])
@@ -842,7 +1306,8 @@ int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
   if (p->min_tgt_head < tr.head_offset || p->max_tgt_head >= tr.head_offset + tr.heads)
     return fail(CB_EINVAL, "target rows hold heads [%d, %d); the plan writes heads %d..%d",
                 tr.head_offset, tr.head_offset + tr.heads, p->min_tgt_head, p->max_tgt_head);
-  if (static_cast<int64_t>(sr.heads) * D > sr.row_stride || static_cast<int64_t>(tr.heads) * D > tr.row_stride)
+  if (static_cast<int64_t>(sr.heads) * D > sr.row_stride ||
+      static_cast<int64_t>(tr.heads) * D > tr.row_stride)
     return fail(CB_EINVAL, "row_stride is smaller than heads * head_dim");
   if (tr.index_kind == CB_INDEX_IDENTITY && sr.index_kind == CB_INDEX_IDENTITY &&
       tr.k_base == sr.k_base && tr.k_base)
@@ -851,25 +1316,34 @@ int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
   int rc;
   if ((rc = to_dev_rows(sr, p->elem_bytes, &a.src))) return rc;
   if ((rc = to_dev_rows(tr, p->elem_bytes, &a.tgt))) return rc;
+  const bool ws = p->info.support == 1;
+  if (ws && (sr.rows > INT32_MAX || tr.rows > INT32_MAX))
+    return fail(CB_EINVAL, "pools with more than 2^31 rows are not supported");
+  const int unit = ws ? kSubTokens : kGenSubTokens;
   int chunk = rq->tokens_per_workgroup;
-  if (chunk == 0) chunk = p->info.support == 1 ? 512 : kSubTokens;
-  if (chunk < kSubTokens || chunk % kSubTokens)
-    return fail(CB_EINVAL, "tokens_per_workgroup must be a positive multiple of %d", kSubTokens);
+  if (chunk == 0) chunk = default_chunk(p, n);
+  if (chunk < unit || chunk % unit)
+    return fail(CB_EINVAL, "tokens_per_workgroup must be a positive multiple of %d", unit);
   a.w = static_cast<const uint4*>(p->d_w);
   a.bias = p->d_bias;
   a.jobs = p->d_jobs;
   a.pairs = p->d_pairs;
-  a.group_of = p->d_group_of;
-  a.group_start = p->d_group_start;
-  a.group_size = p->d_group_size;
+  a.unit_job = p->d_unit_job;
+  a.unit_njobs = p->d_unit_njobs;
+  a.unit_group = p->d_unit_group;
+  a.group_unit_start = p->d_group_unit_start;
+  a.group_unit_count = p->d_group_unit_count;
   a.cos_tab = p->d_cos;
   a.sin_tab = p->d_sin;
+  a.ucos_tab = p->d_ucos;
+  a.usin_tab = p->d_usin;
   a.theta_stride = static_cast<int64_t>(p->info.table_positions) * (D / 2);
   a.n_tokens = n;
   a.position_start = rq->position_start;
   a.support = p->info.support;
   a.chunk = chunk;
   a.err = p->d_err;
+  a.sink = p->d_sink;
   const int64_t prefix = rq->prefix_length > 0 ? rq->prefix_length
                                                : static_cast<int64_t>(rq->position_start) + n;
   if (prefix < static_cast<int64_t>(rq->position_start) + n)
@@ -882,12 +1356,12 @@ int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
     const int64_t first = std::max<int64_t>(0, first_pos - rq->position_start);
     const int64_t count = std::max<int64_t>(0, n - first);
     const int64_t nch = (count + chunk - 1) / chunk;
-    a.cls_job_begin[c] = p->cls_job_begin[c];
+    a.cls_unit_begin[c] = p->cls_unit_begin[c];
     a.cls_tok_first[c] = static_cast<int32_t>(std::min<int64_t>(first, n));
     a.cls_tok_count[c] = static_cast<int32_t>(count);
     a.cls_nchunks[c] = static_cast<int32_t>(std::max<int64_t>(nch, 1));
     a.cls_item_begin[c] = static_cast<int32_t>(items);
-    items += static_cast<int64_t>(p->cls_job_end[c] - p->cls_job_begin[c]) * nch;
+    items += static_cast<int64_t>(p->cls_unit_end[c] - p->cls_unit_begin[c]) * nch;
   }
   a.cls_item_begin[p->num_windows] = static_cast<int32_t>(items);
   if (items == 0) return CB_OK;
@@ -895,12 +1369,22 @@ int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
   a.total_items = static_cast<int32_t>(items);
   a.padded_items = static_cast<int32_t>((items + 7) / 8 * 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 128 && p->ntw == 2)
-    hipLaunchKernelGGL((map_install_kernel<128, uint16_t>), dim3(a.padded_items), dim3(kThreads), 0, s, a);
-  else if (D == 64 && p->ntw == 2)
-    hipLaunchKernelGGL((map_install_kernel<64, uint16_t>), dim3(a.padded_items), dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((map_install_kernel<64, float>), dim3(a.padded_items), dim3(kThreads), 0, s, a);
+  const dim3 grid(a.padded_items), block(ws ? kStreamThreads : kThreads);
+  if (ws) {
+    if (D == 128 && p->ntw == 2)
+      hipLaunchKernelGGL((map_install_stream_kernel<128, uint16_t>), grid, block, 0, s, a);
+    else if (D == 64 && p->ntw == 2)
+      hipLaunchKernelGGL((map_install_stream_kernel<64, uint16_t>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((map_install_stream_kernel<64, float>), grid, block, 0, s, a);
+  } else {
+    if (D == 128 && p->ntw == 2)
+      hipLaunchKernelGGL((map_install_gen_kernel<128, uint16_t>), grid, block, 0, s, a);
+    else if (D == 64 && p->ntw == 2)
+      hipLaunchKernelGGL((map_install_gen_kernel<64, uint16_t>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((map_install_gen_kernel<64, float>), grid, block, 0, s, a);
+  }
   CB_HIP(hipGetLastError());
   return CB_OK;
 }
