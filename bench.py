@@ -65,8 +65,14 @@ def time_handoff(h, steps: int, warmup: int, tokens_per_workgroup: int = 0):
     return wall, statistics.fmean(kernel_ms), min(kernel_ms)
 
 
-def cpu_baseline(workload: str, tokens: int):
-    """CPU oracle (torch fp32, op for op as the reference mapper + row-store install)."""
+def cpu_baseline(workload: str, tokens: int, budget_s: float = 12.0):
+    """CPU oracle (torch fp32, op for op as the reference mapper + row-store install).
+
+    Timed on min(16, affinity) host threads: one warm-up, then repeated full
+    handoffs until ``budget_s`` seconds of work (at least 3), median reported.
+    One single-thread handoff is timed as well (the reference CI's
+    ``OMP_NUM_THREADS=1`` setting).
+    """
     import torch
 
     from cachebridge_amd import synthetic
@@ -74,21 +80,28 @@ def cpu_baseline(workload: str, tokens: int):
 
     cores = min(16, len(os.sched_getaffinity(0)))
     prev = torch.get_num_threads()
-    torch.set_num_threads(cores)
+    sh = synthetic.shape(workload, tokens=tokens)
+    spec = synthetic.mapper_spec(sh)
+    values = synthetic.source_values(sh)
+    src = oi.RowStorePool(sh.source_layers, tokens, sh.source_heads, sh.head_dim, fill=values)
+    tgt = oi.RowStorePool(sh.target_layers, tokens, sh.target_heads, sh.head_dim)
+    slots = torch.randperm(tokens, generator=torch.Generator().manual_seed(5))
+
+    def once() -> float:
+        t0 = time.perf_counter()
+        oi.map_install_oracle(src, torch.arange(tokens), tgt, slots, spec, position_start=0,
+                              source_theta=sh.source_theta, target_thetas=sh.target_theta)
+        return time.perf_counter() - t0
+
     try:
-        sh = synthetic.shape(workload, tokens=tokens)
-        spec = synthetic.mapper_spec(sh)
-        values = synthetic.source_values(sh)
-        src = oi.RowStorePool(sh.source_layers, tokens, sh.source_heads, sh.head_dim, fill=values)
-        tgt = oi.RowStorePool(sh.target_layers, tokens, sh.target_heads, sh.head_dim)
-        slots = torch.randperm(tokens, generator=torch.Generator().manual_seed(5))
+        torch.set_num_threads(cores)
+        once()
         times = []
-        for _ in range(4):
-            t0 = time.perf_counter()
-            oi.map_install_oracle(src, torch.arange(tokens), tgt, slots, spec, position_start=0,
-                                  source_theta=sh.source_theta, target_thetas=sh.target_theta)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times[1:])
+        while len(times) < 3 or sum(times) < budget_s:
+            times.append(once())
+        med = statistics.median(times)
+        torch.set_num_threads(1)
+        single = once()
     finally:
         torch.set_num_threads(prev)
     cpu = ""
@@ -102,7 +115,26 @@ def cpu_baseline(workload: str, tokens: int):
     return {"value": round(tokens / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"full {workload} handoff ({tokens} tokens, all target layers and heads), "
                       f"CPU oracle torch fp32 incl. un-RoPE of all source layers and row-store "
-                      f"install; 1 warm-up + median of 3 ({med:.2f} s each); host CPU: {cpu}"}
+                      f"install; 1 warm-up + median of {len(times)} ({med:.3f} s each); "
+                      f"host CPU: {cpu}",
+            "single_thread_value": round(tokens / single, 1)}
+
+
+def profiled_traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed profiler-counter summary, if any.
+
+    ``profiles/<kernel>_<workload>_traffic.md`` holds a line
+    ``traffic_bytes_per_launch = N`` computed from ``rocprofv3 --pmc FETCH_SIZE``
+    and ``--pmc WRITE_SIZE`` runs of this script, each scaled by the same
+    counter's reading for a plain copy of known size.
+    """
+    path = ROOT / "profiles" / f"{kernel}_{workload}_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch"):
+            return int(line.split("=", 1)[1].strip())
+    return None
 
 
 def copy_calibration(mib: int = 1024, steps: int = 5) -> None:
@@ -180,8 +212,9 @@ def main() -> int:
                    "source_layers": sh.source_layers, "source_kv_heads": sh.source_heads,
                    "head_dim": sh.head_dim, "page_size": sh.page_size},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "map_install_kernel<128, bf16>",
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic("map_install_stream", args.workload),
+                     "kernel": "map_install_stream_kernel<128, bf16>",
                      "algorithmic_bytes_per_launch": bytes_alg,
                      "kernel_ms_mean": round(kernel_ms, 5), "kernel_ms_min": round(kernel_min, 5)},
         "mfma": {"algorithmic_tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 2),

@@ -873,13 +873,19 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
 // Plan tables from standard [theta][pos][D/2] cos/sin: rotation tables and
 // un-rotation tables cos/m, sin/m (m = max(cos^2 + sin^2, FLT_MIN)), both in
 // the permuted half-row layout; also max |m - 1| per theta set (as float bits).
-__global__ void prepare_tables_kernel(const float* __restrict__ c, const float* __restrict__ s,
-                                      float* __restrict__ rc, float* __restrict__ rs,
-                                      float* __restrict__ uc, float* __restrict__ us, int64_t n,
-                                      int half, int64_t per_theta, unsigned* __restrict__ norm_dev) {
+// Grid: (blocks per theta set, theta sets); each block reduces its maximum in
+// LDS and issues one atomic.
+__global__ __launch_bounds__(256) void prepare_tables_kernel(
+    const float* __restrict__ c, const float* __restrict__ s, float* __restrict__ rc,
+    float* __restrict__ rs, float* __restrict__ uc, float* __restrict__ us, int half,
+    int64_t per_theta, unsigned* __restrict__ norm_dev) {
 #pragma clang fp contract(off)
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+  __shared__ unsigned red[256];
+  const int64_t base = static_cast<int64_t>(blockIdx.y) * per_theta;
+  unsigned dev = 0u;
+  for (int64_t k = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; k < per_theta;
+       k += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = base + k;
     const float cc = c[i], ss = s[i];
     const float m = fmaxf(cc * cc + ss * ss, 1.17549435e-38f);
     const int64_t row = i / half;
@@ -888,8 +894,15 @@ __global__ void prepare_tables_kernel(const float* __restrict__ c, const float* 
     rs[o] = ss;
     uc[o] = cc / m;
     us[o] = ss / m;
-    atomicMax(norm_dev + i / per_theta, __float_as_uint(fabsf(m - 1.0f)));
+    dev = max(dev, __float_as_uint(fabsf(m - 1.0f)));
   }
+  red[threadIdx.x] = dev;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + w]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) atomicMax(norm_dev + blockIdx.y, red[0]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1113,8 +1126,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     std::vector<unsigned> norm(d->num_thetas, 0u);
     hipError_t e = hipMemset(d_norm, 0, d->num_thetas * sizeof(unsigned));
     if (e == hipSuccess) {
-      hipLaunchKernelGGL(prepare_tables_kernel, dim3(1024), dim3(256), 0, 0, d->d_cos, d->d_sin,
-                         p->d_cos, p->d_sin, p->d_ucos, p->d_usin, static_cast<int64_t>(table), D / 2,
+      hipLaunchKernelGGL(prepare_tables_kernel, dim3(256, d->num_thetas), dim3(256), 0, 0,
+                         d->d_cos, d->d_sin, p->d_cos, p->d_sin, p->d_ucos, p->d_usin, D / 2,
                          static_cast<int64_t>(d->table_positions) * (D / 2), d_norm);
       e = hipGetLastError();
     }

@@ -105,15 +105,21 @@ class HeadwiseMapper:
         src_h = np.repeat(ah.reshape(lt * ht, s).numpy(), 2, axis=0)
         w = torch.stack((torch.as_tensor(k_weight), torch.as_tensor(v_weight)), dim=2)
         b = torch.stack((torch.as_tensor(k_bias), torch.as_tensor(v_bias)), dim=2)
+        self._jobs = {
+            "job_target_layer": tl, "job_target_head": th, "job_kind": kind,
+            "source_layers": src_l, "source_heads": src_h,
+            "weights": w.reshape(jobs, s * d, d), "biases": b.reshape(jobs, d),
+            "job_source_theta": np.full(jobs, src_theta),
+            "job_target_theta": np.repeat(np.asarray(layer_theta), ht * 2),
+            "job_window": np.repeat(np.asarray(layer_window), ht * 2),
+        }
+        self._theta_sets = theta_sets
+        self._window_sizes = window_sizes
+        self._max_positions = int(max_positions)
         self.plan = HandoffPlan(
-            head_dim=d, dtype=dtype, target_layers=lt, target_heads=ht,
-            job_target_layer=tl, job_target_head=th, job_kind=kind,
-            source_layers=src_l, source_heads=src_h,
-            weights=w.reshape(jobs, s * d, d), biases=b.reshape(jobs, d),
-            thetas=theta_sets, job_source_theta=np.full(jobs, src_theta),
-            job_target_theta=np.repeat(np.asarray(layer_theta), ht * 2),
-            job_window=np.repeat(np.asarray(layer_window), ht * 2),
+            head_dim=d, dtype=dtype, target_layers=lt, target_heads=ht, thetas=theta_sets,
             window_sizes=window_sizes, max_positions=max_positions, device=self.device,
+            **self._jobs,
         )
         self._target_layers = lt
         self._max_source_layer = int(al.max())
@@ -128,6 +134,31 @@ class HeadwiseMapper:
     @property
     def target_layers(self) -> int:
         return self._target_layers
+
+    def layer_plan(self, layers: Sequence[int]) -> HandoffPlan:
+        """A plan for a subset of target layers; its target layer ``i`` is ``layers[i]``.
+
+        Same maps, RoPE settings and window classes as the full plan, so every
+        mapped row is bit-identical to the full plan's (used by the staged
+        layer-chunk pipeline).
+        """
+        layers = [int(l) for l in layers]
+        if not layers or len(set(layers)) != len(layers) or not all(
+                0 <= l < self._target_layers for l in layers):
+            raise ValueError("layer_plan needs distinct target layers of this mapper")
+        tl = self._jobs["job_target_layer"]
+        pick = np.concatenate([np.flatnonzero(tl == l) for l in layers])
+        local = np.empty(self._target_layers, dtype=np.int64)
+        local[layers] = np.arange(len(layers))
+        sub = {k: (v[torch.as_tensor(pick)] if isinstance(v, torch.Tensor) else v[pick])
+               for k, v in self._jobs.items()}
+        sub["job_target_layer"] = local[tl[pick]]
+        return HandoffPlan(
+            head_dim=self.head_dim, dtype=self.dtype, target_layers=len(layers),
+            target_heads=self.local_heads, thetas=self._theta_sets,
+            window_sizes=self._window_sizes, max_positions=self._max_positions,
+            device=self.device, **sub,
+        )
 
     def _check_positions(self, position_start: int, tokens: int) -> None:
         if position_start < 0 or position_start + tokens > self.plan.max_positions:

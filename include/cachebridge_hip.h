@@ -20,21 +20,21 @@
  * never synchronize the device, except plan creation and cb_plan_read_errors.
  *
  * Reference interfaces replaced (paths relative to the reference repository,
- * cb/ = src/cachebridge/):
+ * cb/ = src/cachebridge/, rt/ = src/cachebridge/backends/sglang/runtime/):
  *   cb_plan_create     <- PageMapper.__init__ (cb/mapper.py:35-110): weight
  *                         load + TP head slice, here plus MFMA pre-packing and
  *                         resident RoPE tables (cb/rope.py:16-72).
  *   cb_map_install     <- PageMapper.map_page (cb/mapper.py:117-239) fused with
  *                         map_write_block / set_kv_buffer
  *                         (cb/online/blocks.py:86-111,
- *                         backends/sglang/runtime/r010_core.py:16-43) and the
+ *                         rt/r010_core.py:16-43) and the
  *                         run-segmented install of _DirectMappedPoolCodec
- *                         (backends/sglang/runtime/source_mapper_adapter.py:366-428).
+ *                         (rt/source_mapper_adapter.py:366-428).
  *                         With an identity target index it is map_page's
  *                         dense [2, Lt, n, Ht, D] output (cb/mapper.py:216-239).
  *   cb_copy_rows       <- pack_source_block (cb/online/blocks.py:47-82) and the
  *                         per-run install copies of _DirectMappedPoolCodec.copy
- *                         (source_mapper_adapter.py:400-420).
+ *                         (rt/source_mapper_adapter.py:400-420).
  */
 #ifndef CACHEBRIDGE_HIP_H
 #define CACHEBRIDGE_HIP_H

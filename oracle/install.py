@@ -5,7 +5,7 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 - ``RowStorePool``: SGLang ``MHATokenToKVPool`` duck type (``layer_num``,
   ``start_layer``, ``dtype``, ``_get_key_buffer``, ``_get_value_buffer``,
   ``set_kv_buffer``) as consumed at ``cb/online/blocks.py:57-59,79-81,106-111``
-  and ``backends/sglang/runtime/r010_core.py:37-43``. SGLang v0.4.10.post2
+  and ``cb/backends/sglang/runtime/r010_core.py:37-43``. SGLang v0.4.10.post2
   (commit 8cd344586e09669432d35c678b7cc208c0a6f47e) is an un-vendored
   dependency; its ``set_kv_buffer`` is restated as a plain row store
   ``buffer[layer][loc] = k.to(dtype)``. PARITY UNPINNED against SGLang itself

@@ -31,6 +31,17 @@ def golden_dir():
     return GOLDEN
 
 
+@pytest.fixture(scope="session")
+def built_library():
+    """The in-tree HIP library; compiled here if a fresh checkout has none."""
+    from cachebridge_amd import _lib
+    from cachebridge_amd.build import build_library
+
+    if not _lib.LIB_PATH.exists():
+        build_library()
+    return _lib.LIB_PATH
+
+
 @pytest.fixture(autouse=True)
 def _single_thread_cpu():
     # Oracle arithmetic runs single-threaded so torch's vectorized kernels see
