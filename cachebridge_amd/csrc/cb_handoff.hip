@@ -83,6 +83,7 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kMaxClasses = CB_MAX_WINDOW_CLASSES;
+constexpr int kMaxStreamBlocks = 256;  // streaming-kernel workgroups (one per CU)
 
 // ---------------------------------------------------------------------------
 // Element helpers
@@ -249,6 +250,38 @@ __device__ inline int64_t row_of(const DevRows& R, int t) {
   }
 }
 
+// row_of in two steps, so the loaded index is not consumed in the iteration
+// that loads it. row_fetch issues exactly two 4-byte loads for every index
+// kind (addresses chosen by uniform selects; words an index kind does not
+// need read `spare`, any valid device word), so the loop's memory-operation
+// count is static and nothing waits on the loads; row_finish (one iteration
+// later) assembles the row: identity u, int32 slot, int64 slot, or block
+// table entry * page_size + u % page_size.
+__device__ inline uint2 row_fetch(const DevRows& R, int t, const CB_GLOBAL uint32_t* spare) {
+  const int64_t u = t + R.index_offset;
+  const uint32_t ps = static_cast<uint32_t>(R.page_size > 0 ? R.page_size : 1);
+  const CB_GLOBAL uint32_t* idx =
+      R.index ? reinterpret_cast<const CB_GLOBAL uint32_t*>(as_global(R.index)) : spare;
+  const int k = R.index_kind;
+  const int64_t w0 = k == CB_INDEX_I64 ? 2 * u : k == CB_INDEX_I32 ? u : static_cast<uint32_t>(u) / ps;
+  const CB_GLOBAL uint32_t* p0 = k == CB_INDEX_IDENTITY ? spare : idx + w0;
+  const CB_GLOBAL uint32_t* p1 = k == CB_INDEX_I64 ? idx + w0 + 1 : spare;
+  return make_uint2(*p0, *p1);
+}
+
+__device__ inline int64_t row_finish(const DevRows& R, int t, uint2 f) {
+  const int64_t u = t + R.index_offset;
+  switch (R.index_kind) {
+    case CB_INDEX_IDENTITY: return u;
+    case CB_INDEX_I32: return static_cast<int32_t>(f.x);
+    case CB_INDEX_I64: return static_cast<int64_t>((static_cast<uint64_t>(f.y) << 32) | f.x);
+    default: {
+      const uint32_t ps = static_cast<uint32_t>(R.page_size);
+      return static_cast<int64_t>(static_cast<int32_t>(f.x)) * ps + static_cast<uint32_t>(u) % ps;
+    }
+  }
+}
+
 __device__ inline gcptr layer_base(const DevRows& R, int kind, int layer) {
   const void* const* arr = kind ? R.v_layers : R.k_layers;
   if (arr) return as_global(*reinterpret_cast<const CB_GLOBAL void* const CB_GLOBAL*>(as_global(arr + layer)));
@@ -288,6 +321,17 @@ struct MapArgs {
   int32_t cls_item_begin[kMaxClasses + 1];
   int32_t total_items;
   int32_t padded_items;
+  // Streaming kernel: cost-balanced ranges (one workgroup per CU).
+  const int32_t* unit_cost_prefix;  // [units + 1] prefix sums of per-unit cost weights
+  int32_t cls_unit_end[kMaxClasses];
+  int32_t cls_subtiles[kMaxClasses];     // 16-token sub-tiles of each class's tokens
+  int64_t cls_cost_begin[kMaxClasses + 1];
+  int32_t num_units;
+  int32_t num_blocks;
+  // Range r of the cost line covers (unit, sub-tile) from blk_unit/sub[r] to
+  // blk_unit/sub[r + 1] (computed on the host with cost_to_pos).
+  int32_t blk_unit[kMaxStreamBlocks + 1];
+  int32_t blk_sub[kMaxStreamBlocks + 1];
   int32_t* err;
   void* sink;  // scratch destination of stores without a target row
 };
@@ -322,6 +366,43 @@ __device__ inline bool decode_work(const MapArgs& a, Work* w) {
   w->tok_lo = a.cls_tok_first[c] + chunk_id * a.chunk;
   w->tok_hi = min(w->tok_lo + a.chunk, a.cls_tok_first[c] + a.cls_tok_count[c]);
   return true;
+}
+
+// Streaming kernel work split. Every (unit, 16-token sub-tile) has a cost
+// weight (the unit's kind and job count); the weights laid end to end, class
+// by class, form one cost line that is cut into num_blocks equal ranges. A
+// cut at cost P falls in sub-tile floor((P - unit start) / weight) of its
+// unit, so neighbouring ranges share the cut and tile the work exactly.
+// Workgroup b takes range (b & 7) * (num_blocks / 8) + (b >> 3): each XCD
+// owns one contiguous eighth of the cost line, so units that read the same
+// source rows (adjacent in the unit order) share that XCD's L2.
+struct Pos {
+  int unit, sub;
+};
+static_assert(sizeof(MapArgs) <= 4096, "kernel arguments must fit 4 KB");
+
+__host__ __device__ inline Pos cost_to_pos(const MapArgs& a, int64_t P) {
+  if (P >= a.cls_cost_begin[a.ncls]) return Pos{a.num_units, 0};
+  int c = 0;
+  while (c + 1 < a.ncls && P >= a.cls_cost_begin[c + 1]) ++c;
+  const int64_t q = P - a.cls_cost_begin[c];
+  const int64_t ns = a.cls_subtiles[c];
+  const int ub = a.cls_unit_begin[c];
+  const int64_t base = a.unit_cost_prefix[ub];
+  int lo = ub, hi = a.cls_unit_end[c] - 1;  // largest u with (prefix[u] - base) * ns <= q
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((a.unit_cost_prefix[mid] - base) * ns <= q) lo = mid;
+    else hi = mid - 1;
+  }
+  const int64_t w = a.unit_cost_prefix[lo + 1] - a.unit_cost_prefix[lo];
+  return Pos{lo, static_cast<int>((q - (a.unit_cost_prefix[lo] - base) * ns) / w)};
+}
+
+__host__ __device__ inline int class_of_unit(const MapArgs& a, int u) {
+  int c = 0;
+  while (c + 1 < a.ncls && u >= a.cls_unit_end[c]) ++c;
+  return c;
 }
 
 // MFMA product schedule: term pairs (i of x, j of w) with i + j < NTW, small first.
@@ -371,7 +452,6 @@ constexpr int kUnitJobs = 2;                     // jobs per streaming unit
 constexpr int kStreamWaves = 8;
 constexpr int kStreamThreads = kWave * kStreamWaves;
 constexpr int kSubTokens = 16;                   // tokens per wave sub-tile
-constexpr int kRowSegment = 2048;                // tokens whose rows are staged in LDS at once
 constexpr int kSinkBytes = kWave * 128 * 4;       // one head row (D <= 128, fp32) per lane
 
 __host__ __device__ inline int gen_out_dim(int D, int rt, int r) {
@@ -380,10 +460,10 @@ __host__ __device__ inline int gen_out_dim(int D, int rt, int r) {
 }
 
 // Stage NU4 uint4 into LDS with NT threads (NU4 a multiple of NT).
-template <int NU4, int NT>
+template <int NU4, int NT, int MAXB = 8>
 __device__ inline void copy_to_lds(uint4* lds, const uint4* __restrict__ src) {
   constexpr int PER = NU4 / NT;
-  constexpr int B = PER < 8 ? PER : 8;
+  constexpr int B = PER < MAXB ? PER : MAXB;
   static_assert(NU4 % NT == 0 && PER % B == 0, "block size");
   for (int base = 0; base < NU4; base += NT * B) {
     uint4 v[B];
@@ -409,8 +489,7 @@ struct Gm {
 };
 
 template <int D, typename IO, bool IS_K, bool SHARED, int NJ>
-__device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int32_t* lds_rows,
-                           const Work& wk) {
+__device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, const Work& wk) {
   using C = Gm<D, IO>;
   using T = IOTraits<IO>;
   constexpr int NTW = C::NTW;
@@ -443,201 +522,261 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int3
   // iteration issues a fixed number of memory operations (the compiler can
   // then wait for the prefetched loads without also waiting for the stores).
   gptr sink = as_global(a.sink) + lane * (D * C::BYTES);
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    copy_to_lds<C::W_U4, kStreamThreads>(lds_w + j * C::W_U4, a.w + static_cast<size_t>(wk.job + j) * C::W_U4);
-    if (threadIdx.x < D) lds_bias[j * D + threadIdx.x] = a.bias[static_cast<size_t>(wk.job + j) * D + threadIdx.x];
-  }
 
   gcptr sbase = layer_base(a.src, kind, sl) + static_cast<int64_t>(sh - a.src.head_offset) * D * C::BYTES;
   const CB_GLOBAL float* ucos = gtab(SHARED ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
   const CB_GLOBAL float* usin = gtab(SHARED ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
   const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
   const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
-  int32_t* srows = lds_rows;
-  int32_t* trows = lds_rows + kRowSegment;
 
-  for (int seg = wk.tok_lo; seg < wk.tok_hi; seg += kRowSegment) {
-    const int seg_n = min(kRowSegment, wk.tok_hi - seg);
-    // Source and target rows of the segment's tokens (-1: skip), so that the
-    // streaming loop issues no dependent index loads.
-    __syncthreads();
-    for (int i = threadIdx.x; i < seg_n; i += kStreamThreads) {
-      const int64_t s = row_of(a.src, seg + i);
-      const int64_t d = row_of(a.tgt, seg + i);
-      const bool sok = s >= 0 && s < a.src.rows;
-      const bool dok = d >= 0 && d < a.tgt.rows;
-      if (!sok) atomicOr(a.err, 1);
-      if (!dok) atomicOr(a.err, 2);
-      srows[i] = sok ? static_cast<int32_t>(s) : -1;
-      trows[i] = dok ? static_cast<int32_t>(d) : -1;
+  const int n = wk.tok_hi - wk.tok_lo;
+  const int nsub = (n + kSubTokens - 1) / kSubTokens;
+  int errbits = 0;
+  // Source and target rows of this lane's token in sub-tile `sub` (-1: skip).
+  // The index loads are issued two sub-tiles ahead (fetch) and resolved one
+  // sub-tile ahead (finish); tokens past the range re-read the range's last
+  // token and are masked.
+  auto token_of = [&](int sub) { return wk.tok_lo + min(sub * kSubTokens + col, n - 1); };
+  const CB_GLOBAL uint32_t* spare = reinterpret_cast<const CB_GLOBAL uint32_t*>(as_global(a.sink));
+  auto fetch_rows = [&](int sub, uint2& fs, uint2& fd) {
+    fs = row_fetch(a.src, token_of(sub), spare);
+    fd = row_fetch(a.tgt, token_of(sub), spare);
+  };
+  auto finish_rows = [&](int sub, uint2 fs, uint2 fd, int32_t& sr, int32_t& tr) {
+    const int t = token_of(sub);
+    const int64_t s = row_finish(a.src, t, fs);
+    const int64_t d = row_finish(a.tgt, t, fd);
+    const bool live = sub * kSubTokens + col < n;
+    const bool sok = s >= 0 && s < a.src.rows;
+    const bool dok = d >= 0 && d < a.tgt.rows;
+    errbits |= live ? (sok ? 0 : 1) | (dok ? 0 : 2) : 0;
+    sr = live && sok ? static_cast<int32_t>(s) : -1;
+    tr = live && dok ? static_cast<int32_t>(d) : -1;
+  };
+
+  uint4 xr[2][C::RUN_U4];           // raw source dims of the next sub-tile: [half][16 B]
+  float uc[TG], us[TG];             // its un-rotation table values
+  int32_t row_next = -1;
+  auto prefetch = [&](int sub, int32_t srow) {
+    const int i = sub * kSubTokens + col;
+    row_next = srow;
+    {
+      // Rows without a source read row 0 (always valid) and are zeroed on use.
+      const int64_t r = srow >= 0 ? srow : 0;
+      gcptr p = sbase + r * a.src.row_stride_b + g * G * C::BYTES;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int u = 0; u < C::RUN_U4; ++u)
+          xr[h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
     }
-    __syncthreads();
+    if constexpr (IS_K) {
+      const int64_t off = static_cast<int64_t>(a.position_start + wk.tok_lo + min(i, n - 1)) * HALF;
+      load_tab<G>(ucos + off, g, uc);
+      load_tab<G>(usin + off, g, us);
+    }
+  };
 
-    const int nsub = (seg_n + kSubTokens - 1) / kSubTokens;
-    uint4 xr[2][C::RUN_U4];           // raw source dims of the next sub-tile: [half][16 B]
-    float uc[TG], us[TG];             // its un-rotation table values
-    int32_t row_next = -1;
-    auto prefetch = [&](int sub) {
-      const int i = sub * kSubTokens + col;
-      row_next = (sub < nsub && i < seg_n) ? srows[i] : -1;
-      {
-        // Rows without a source read row 0 (always valid) and are zeroed on use.
-        const int64_t r = row_next >= 0 ? row_next : 0;
-        gcptr p = sbase + r * a.src.row_stride_b + g * G * C::BYTES;
+  // Segment start: the unit's W and bias, the first rows and the first
+  // sub-tile are loaded before waiting for the workgroup's previous segment
+  // to release LDS, so their latency overlaps that segment's tail.
+  int sub = wave;
+  int32_t sr_a, tr_a, sr_b, tr_b;
+  uint2 fs, fd;
+  fetch_rows(sub, fs, fd);
+  constexpr int WTOT = NJ * C::W_U4;
+  constexpr int WPER = (WTOT + kStreamThreads - 1) / kStreamThreads;
+  static_assert(NJ * D <= kStreamThreads, "staging split");
+  uint4 wreg[WPER];
+  {
+    gcptr wsrc = as_global(a.w + static_cast<size_t>(wk.job) * C::W_U4);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+    for (int i = 0; i < WPER; ++i) {
+      const int e = i * kStreamThreads + threadIdx.x;
+      wreg[i] = (WTOT % kStreamThreads == 0 || e < WTOT) ? gload<uint4>(wsrc + e * 16) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  const float breg = threadIdx.x < NJ * D ? a.bias[static_cast<size_t>(wk.job) * D + threadIdx.x] : 0.f;
+  finish_rows(sub, fs, fd, sr_a, tr_a);
+  prefetch(sub, sr_a);
+  fetch_rows(sub + kStreamWaves, fs, fd);
+  __syncthreads();  // the previous segment no longer reads LDS
 #pragma unroll
-          for (int u = 0; u < C::RUN_U4; ++u)
-            xr[h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
+  for (int i = 0; i < WPER; ++i) {
+    const int e = i * kStreamThreads + threadIdx.x;
+    if (WTOT % kStreamThreads == 0 || e < WTOT) lds_w[e] = wreg[i];
+  }
+  if (threadIdx.x < NJ * D) lds_bias[threadIdx.x] = breg;
+  __syncthreads();  // W and bias staged
+  // Enter the loop with the memory operations of one iteration outstanding in
+  // the same order (x and tables, row indices, NJ row stores; the stores go to
+  // the sink), so the compiler's waits inside the loop only cover the loads
+  // they need instead of draining every outstanding operation.
+  {
+    float zero[G];
+#pragma unroll
+    for (int e = 0; e < G; ++e) zero[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      store_elems<IO, G>(sink + (g * G) * C::BYTES, zero);
+      store_elems<IO, G>(sink + (HALF + g * G) * C::BYTES, zero);
+    }
+  }
+  for (; sub < nsub; sub += kStreamWaves) {
+    // W fragments are re-read from LDS every sub-tile: keep the compiler from
+    // hoisting all of them into registers.
+    asm volatile("" ::: "memory");
+    const int i = sub * kSubTokens + col;
+    const int64_t trow = tr_a;
+    const bool have = row_next >= 0;
+
+    // Un-rotate (keys) and split the current sub-tile into B fragments.
+    bf16x8 bx[KS][XT];
+    float tc[SHARED ? G : 1], ts[SHARED ? G : 1];
+    {
+      float x1[G], x2[G];
+#pragma unroll
+      for (int u = 0; u < C::RUN_U4; ++u) {
+        unpack16<IO>(xr[0][u], x1 + u * C::E16);
+        unpack16<IO>(xr[1][u], x2 + u * C::E16);
       }
       if constexpr (IS_K) {
-        const int64_t off = static_cast<int64_t>(a.position_start + seg + min(i, seg_n - 1)) * HALF;
-        load_tab<G>(ucos + off, g, uc);
-        load_tab<G>(usin + off, g, us);
-      }
-    };
-
-    int sub = wave;
-    prefetch(sub);
-    for (; sub < nsub; sub += kStreamWaves) {
-      // W fragments are re-read from LDS every sub-tile: keep the compiler from
-      // hoisting all of them into registers.
-      asm volatile("" ::: "memory");
-      const int i = sub * kSubTokens + col;
-      const int64_t trow = i < seg_n ? trows[i] : -1;
-      const bool have = row_next >= 0;
-
-      // Un-rotate (keys) and split the current sub-tile into B fragments.
-      bf16x8 bx[KS][XT];
-      float tc[SHARED ? G : 1], ts[SHARED ? G : 1];
-      {
-        float x1[G], x2[G];
 #pragma unroll
-        for (int u = 0; u < C::RUN_U4; ++u) {
-          unpack16<IO>(xr[0][u], x1 + u * C::E16);
-          unpack16<IO>(xr[1][u], x2 + u * C::E16);
+        for (int e = 0; e < G; ++e) {
+          const float k1 = x1[e] * uc[e] + x2[e] * us[e];
+          const float k2 = x2[e] * uc[e] - x1[e] * us[e];
+          x1[e] = k1;
+          x2[e] = k2;
         }
-        if constexpr (IS_K) {
+        if constexpr (SHARED) {
 #pragma unroll
           for (int e = 0; e < G; ++e) {
-            const float k1 = x1[e] * uc[e] + x2[e] * us[e];
-            const float k2 = x2[e] * uc[e] - x1[e] * us[e];
-            x1[e] = k1;
-            x2[e] = k2;
+            tc[e] = uc[e];
+            ts[e] = us[e];
           }
-          if constexpr (SHARED) {
-#pragma unroll
-            for (int e = 0; e < G; ++e) {
-              tc[e] = uc[e];
-              ts[e] = us[e];
-            }
-          }
-        }
-        if (!have) {
-#pragma unroll
-          for (int e = 0; e < G; ++e) x1[e] = x2[e] = 0.f;
-        }
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const float* src = (ks / (KS / 2) ? x2 : x1) + (ks % (KS / 2)) * 8;
-          uint32_t tw[XT][4];
-          split_terms<XT, 8>(src, tw);
-#pragma unroll
-          for (int x = 0; x < XT; ++x)
-            bx[ks][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
         }
       }
-      // Next sub-tile's rows and tables load while this one is multiplied.
-      prefetch(sub + kStreamWaves);
+      if (!have) {
+#pragma unroll
+        for (int e = 0; e < G; ++e) x1[e] = x2[e] = 0.f;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const float* src = (ks / (KS / 2) ? x2 : x1) + (ks % (KS / 2)) * 8;
+        uint32_t tw[XT][4];
+        split_terms<XT, 8>(src, tw);
+#pragma unroll
+        for (int x = 0; x < XT; ++x)
+          bx[ks][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
+      }
+    }
+    // Next sub-tile's source rows and tables load while this one is
+    // multiplied; the index loads of the sub-tile after it are issued too.
+    finish_rows(sub + kStreamWaves, fs, fd, sr_b, tr_b);
+    prefetch(sub + kStreamWaves, sr_b);
+    tr_a = tr_b;
+    fetch_rows(sub + 2 * kStreamWaves, fs, fd);
 
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const uint4* wj = lds_w + j * C::W_U4;
-        f32x4 acc[RT];
+    for (int j = 0; j < NJ; ++j) {
+      const uint4* wj = lds_w + j * C::W_U4;
+      f32x4 acc[RT];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const float* b = lds_bias + j * D + gen_out_dim(D, rt, 4 * g);
-          acc[rt] = f32x4{b[0], b[1], b[2], b[3]};
-        }
-        // W fragments of row tile rt+1 are read from LDS while rt multiplies.
-        bf16x8 aw[2][KS][NTW];
-        auto read_w = [&](int rt, bf16x8 (&dst)[KS][NTW]) {
+      for (int rt = 0; rt < RT; ++rt) {
+        const float* b = lds_bias + j * D + gen_out_dim(D, rt, 4 * g);
+        acc[rt] = f32x4{b[0], b[1], b[2], b[3]};
+      }
+      // W fragments of row tile rt+1 are read from LDS while rt multiplies.
+      bf16x8 aw[2][KS][NTW];
+      auto read_w = [&](int rt, bf16x8 (&dst)[KS][NTW]) {
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
+        for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int w = 0; w < NTW; ++w)
-              dst[ks][w] = __builtin_bit_cast(bf16x8, wj[((rt * KS + ks) * NTW + w) * kWave + lane]);
-        };
-        read_w(0, aw[0]);
+          for (int w = 0; w < NTW; ++w)
+            dst[ks][w] = __builtin_bit_cast(bf16x8, wj[((rt * KS + ks) * NTW + w) * kWave + lane]);
+      };
+      read_w(0, aw[0]);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          if (rt + 1 < RT) read_w(rt + 1, aw[(rt + 1) & 1]);
-          // Keep the reads above this row tile's MFMAs so they stay in flight.
-          __builtin_amdgcn_sched_barrier(0);
+      for (int rt = 0; rt < RT; ++rt) {
+        if (rt + 1 < RT) read_w(rt + 1, aw[(rt + 1) & 1]);
+        // Keep the reads above this row tile's MFMAs so they stay in flight.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-            for_products<XT, NTW>([&](int ii, int jj) { acc[rt] = mfma(aw[rt & 1][ks][jj], bx[ks][ii], acc[rt]); });
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int ks = 0; ks < KS; ++ks)
+          for_products<XT, NTW>([&](int ii, int jj) { acc[rt] = mfma(aw[rt & 1][ks][jj], bx[ks][ii], acc[rt]); });
+        __builtin_amdgcn_sched_barrier(0);
+      }
 
-        // Epilogue: target RoPE (keys), cast, scatter.
-        {
-          float o1[G], o2[G];
+      // Epilogue: target RoPE (keys), cast, scatter.
+      {
+        float o1[G], o2[G];
 #pragma unroll
-          for (int rt = 0; rt < RT / 2; ++rt)
+        for (int rt = 0; rt < RT / 2; ++rt)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              o1[4 * rt + q] = acc[rt][q];
-              o2[4 * rt + q] = acc[rt + RT / 2][q];
-            }
-          if constexpr (IS_K) {
-            float cbuf[G], sbuf[G];
-            const float* c = tc;
-            const float* s = ts;
-            if constexpr (!SHARED) {
-              const int64_t off = static_cast<int64_t>(a.position_start + seg + i) * HALF;
-              load_tab<G>(rcos + off, g, cbuf);
-              load_tab<G>(rsin + off, g, sbuf);
-              c = cbuf;
-              s = sbuf;
-            }
-#pragma unroll
-            for (int e = 0; e < G; ++e) {
-              const float y1 = o1[e], y2 = o2[e];
-              o1[e] = y1 * c[e] - y2 * s[e];
-              o2[e] = y2 * c[e] + y1 * s[e];
-            }
+          for (int q = 0; q < 4; ++q) {
+            o1[4 * rt + q] = acc[rt][q];
+            o2[4 * rt + q] = acc[rt + RT / 2][q];
           }
-          gptr p = trow >= 0 ? tbase[j] + trow * a.tgt.row_stride_b : sink;
-          store_elems<IO, G>(p + (g * G) * C::BYTES, o1);
-          store_elems<IO, G>(p + (HALF + g * G) * C::BYTES, o2);
+        if constexpr (IS_K) {
+          float cbuf[G], sbuf[G];
+          const float* c = tc;
+          const float* s = ts;
+          if constexpr (!SHARED) {
+            const int64_t off = static_cast<int64_t>(a.position_start + wk.tok_lo + min(i, n - 1)) * HALF;
+            load_tab<G>(rcos + off, g, cbuf);
+            load_tab<G>(rsin + off, g, sbuf);
+            c = cbuf;
+            s = sbuf;
+          }
+#pragma unroll
+          for (int e = 0; e < G; ++e) {
+            const float y1 = o1[e], y2 = o2[e];
+            o1[e] = y1 * c[e] - y2 * s[e];
+            o2[e] = y2 * c[e] + y1 * s[e];
+          }
         }
+        gptr p = trow >= 0 ? tbase[j] + trow * a.tgt.row_stride_b : sink;
+        store_elems<IO, G>(p + (g * G) * C::BYTES, o1);
+        store_elems<IO, G>(p + (HALF + g * G) * C::BYTES, o2);
       }
     }
   }
+  if (errbits) atomicOr(a.err, errbits);
 }
 
 template <int D, typename IO>
 __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapArgs a) {
   __shared__ uint4 lds_w[kUnitJobs * Gm<D, IO>::W_U4];
   __shared__ float lds_bias[kUnitJobs * D];
-  __shared__ int32_t lds_rows[2 * kRowSegment];
-  Work wk;
-  if (!decode_work(a, &wk)) return;
-  const int4 meta = a.jobs[wk.job];
-  const bool two = wk.njobs == 2;
-  if ((meta.y & 0xff) == CB_KIND_K) {
-    if (meta.z & kJobSharedTables) {
-      if (two) stream_run<D, IO, true, true, 2>(a, lds_w, lds_bias, lds_rows, wk);
-      else stream_run<D, IO, true, true, 1>(a, lds_w, lds_bias, lds_rows, wk);
-    } else {
-      if (two) stream_run<D, IO, true, false, 2>(a, lds_w, lds_bias, lds_rows, wk);
-      else stream_run<D, IO, true, false, 1>(a, lds_w, lds_bias, lds_rows, wk);
+  const int per = a.num_blocks >> 3;
+  const int r = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  Pos cur{a.blk_unit[r], a.blk_sub[r]};
+  const Pos end{a.blk_unit[r + 1], a.blk_sub[r + 1]};
+  while (cur.unit < end.unit || (cur.unit == end.unit && cur.sub < end.sub)) {
+    const int c = class_of_unit(a, cur.unit);
+    const int stop = cur.unit == end.unit ? end.sub : a.cls_subtiles[c];
+    if (stop > cur.sub) {
+      Work wk;
+      wk.job = a.unit_job[cur.unit];
+      wk.njobs = a.unit_njobs[cur.unit];
+      wk.tok_lo = a.cls_tok_first[c] + cur.sub * kSubTokens;
+      wk.tok_hi = min(a.cls_tok_first[c] + stop * kSubTokens, a.cls_tok_first[c] + a.cls_tok_count[c]);
+      const int4 meta = a.jobs[wk.job];
+      const bool two = wk.njobs == 2;
+      if ((meta.y & 0xff) == CB_KIND_K) {
+        if (meta.z & kJobSharedTables) {
+          if (two) stream_run<D, IO, true, true, 2>(a, lds_w, lds_bias, wk);
+          else stream_run<D, IO, true, true, 1>(a, lds_w, lds_bias, wk);
+        } else {
+          if (two) stream_run<D, IO, true, false, 2>(a, lds_w, lds_bias, wk);
+          else stream_run<D, IO, true, false, 1>(a, lds_w, lds_bias, wk);
+        }
+      } else {
+        if (two) stream_run<D, IO, false, false, 2>(a, lds_w, lds_bias, wk);
+        else stream_run<D, IO, false, false, 1>(a, lds_w, lds_bias, wk);
+      }
     }
-  } else {
-    if (two) stream_run<D, IO, false, false, 2>(a, lds_w, lds_bias, lds_rows, wk);
-    else stream_run<D, IO, false, false, 1>(a, lds_w, lds_bias, lds_rows, wk);
+    cur = Pos{cur.unit + 1, 0};
   }
 }
 
@@ -971,6 +1110,12 @@ struct cb_plan {
   int32_t* d_unit_group = nullptr;
   int32_t* d_group_unit_start = nullptr;
   int32_t* d_group_unit_count = nullptr;
+  int32_t* d_unit_cost_prefix = nullptr;
+  int num_units = 0;
+  int num_cus = 256;
+  std::vector<int32_t> h_unit_cost_prefix;
+  int64_t cls_unit_weight_begin[kMaxClasses] = {0, 0, 0, 0};  // unit cost prefix at class bounds
+  int64_t cls_unit_weight_end[kMaxClasses] = {0, 0, 0, 0};
   float* d_cos = nullptr;
   float* d_sin = nullptr;
   float* d_ucos = nullptr;
@@ -986,7 +1131,7 @@ void plan_free(cb_plan* p) {
   void* ptrs[] = {p->d_w,         p->d_bias,         p->d_jobs,           p->d_pairs,
                   p->d_unit_job,  p->d_unit_njobs,   p->d_unit_group,     p->d_group_unit_start,
                   p->d_group_unit_count, p->d_cos,   p->d_sin,            p->d_ucos,
-                  p->d_usin,      p->d_err,          p->d_sink};
+                  p->d_usin,      p->d_err,          p->d_sink,           p->d_unit_cost_prefix};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
   delete p;
@@ -1099,6 +1244,12 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   }
   for (int c = 0; c < d->num_windows; ++c)
     if (p->cls_unit_begin[c] < 0) p->cls_unit_begin[c] = p->cls_unit_end[c] = 0;
+  p->num_units = static_cast<int>(unit_job.size());
+  {
+    int cus = 0;
+    CB_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device));
+    p->num_cus = std::max(8, std::min(cus, kMaxStreamBlocks) / 8 * 8);
+  }
 
   const size_t w_elems = static_cast<size_t>(nj) * S * (D / 16) * (D / 32) * p->ntw * kWave * 8;
   const size_t table = static_cast<size_t>(d->num_thetas) * d->table_positions * (D / 2);
@@ -1141,6 +1292,25 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
       if (sth == tth && dev <= 2.4e-7f) jobs[i].z |= kJobSharedTables;
     }
     if ((rc = upload(&p->d_jobs, jobs.data(), jobs.size() * sizeof(int4), &bytes))) return rc;
+  }
+  // Relative cost of one 16-token sub-tile of each unit (streaming kernel):
+  // a per-kind base (gather; keys also un-rotate and read tables) plus a
+  // per-job part (MFMAs, epilogue, stores). Keys cost ~1.4x values.
+  {
+    std::vector<int32_t> prefix(unit_job.size() + 1, 0);
+    for (size_t u = 0; u < unit_job.size(); ++u) {
+      const int4 m = jobs[unit_job[u]];
+      const bool key = (m.y & 0xff) == CB_KIND_K;
+      int w = (key ? 6 : 2) + 4 * unit_njobs[u];
+      if (key && !(m.z & kJobSharedTables)) w += 2;
+      prefix[u + 1] = prefix[u] + w;
+    }
+    if ((rc = upload(&p->d_unit_cost_prefix, prefix.data(), prefix.size() * 4, &bytes))) return rc;
+    p->h_unit_cost_prefix = prefix;
+    for (int c = 0; c < d->num_windows; ++c) {
+      p->cls_unit_weight_begin[c] = prefix[p->cls_unit_begin[c]];
+      p->cls_unit_weight_end[c] = prefix[p->cls_unit_end[c]];
+    }
   }
   int32_t* d_order = nullptr;
   CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), order.size() * 4));
@@ -1381,8 +1551,37 @@ int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
   if (items > (int64_t{1} << 30)) return fail(CB_EINVAL, "request too large for one launch");
   a.total_items = static_cast<int32_t>(items);
   a.padded_items = static_cast<int32_t>((items + 7) / 8 * 8);
+  int64_t grid_blocks = a.padded_items;
+  if (ws) {
+    // Cost line: class by class, unit weight x sub-tiles of the class.
+    int64_t cost = 0, unit_tokens = 0;
+    for (int c = 0; c < p->num_windows; ++c) {
+      const int64_t sub = (static_cast<int64_t>(a.cls_tok_count[c]) + kSubTokens - 1) / kSubTokens;
+      a.cls_unit_end[c] = p->cls_unit_end[c];
+      a.cls_subtiles[c] = static_cast<int32_t>(sub);
+      a.cls_cost_begin[c] = cost;
+      cost += (p->cls_unit_weight_end[c] - p->cls_unit_weight_begin[c]) * sub;
+      unit_tokens += static_cast<int64_t>(p->cls_unit_end[c] - p->cls_unit_begin[c]) * a.cls_tok_count[c];
+    }
+    a.cls_cost_begin[p->num_windows] = cost;
+    if (cost == 0) return CB_OK;
+    a.unit_cost_prefix = p->d_unit_cost_prefix;
+    a.num_units = p->num_units;
+    int64_t nb = p->num_cus;
+    if (rq->tokens_per_workgroup > 0)  // cap on unit-tokens per workgroup
+      nb = std::min<int64_t>(nb, std::max<int64_t>(8, (unit_tokens + chunk - 1) / chunk));
+    a.num_blocks = static_cast<int32_t>(std::max<int64_t>(8, nb / 8 * 8));
+    grid_blocks = a.num_blocks;
+    MapArgs host = a;  // cost_to_pos reads the prefix through the args
+    host.unit_cost_prefix = p->h_unit_cost_prefix.data();
+    for (int r = 0; r <= a.num_blocks; ++r) {
+      const Pos q = cost_to_pos(host, cost * r / a.num_blocks);
+      a.blk_unit[r] = q.unit;
+      a.blk_sub[r] = q.sub;
+    }
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(a.padded_items), block(ws ? kStreamThreads : kThreads);
+  const dim3 grid(static_cast<unsigned>(grid_blocks)), block(ws ? kStreamThreads : kThreads);
   if (ws) {
     if (D == 128 && p->ntw == 2)
       hipLaunchKernelGGL((map_install_stream_kernel<128, uint16_t>), grid, block, 0, s, a);
