@@ -28,6 +28,7 @@
 #include <cstring>
 #include <numeric>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/cachebridge_hip.h"
@@ -488,16 +489,22 @@ struct Gm {
   static constexpr int W_U4 = RT * KS * NTW * kWave;
 };
 
-template <int D, typename IO, bool IS_K, bool SHARED, int NJ>
-__device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, const Work& wk) {
+template <int D, typename IO, bool IS_K, bool SHARED, int NJ, int CT>
+__device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int* lds_next, const Work& wk) {
+  // Separately rounded products and sums (as the reference's torch ops), so
+  // every instantiation rounds identically: a job's rows are bit-identical
+  // whichever unit shape or plan computes them.
+#pragma clang fp contract(off)
   using C = Gm<D, IO>;
   using T = IOTraits<IO>;
   constexpr int NTW = C::NTW;
   constexpr int XT = IS_K ? T::XT_K : T::XT_V;
   constexpr int KS = C::KS, RT = C::RT, G = C::G, HALF = C::HALF;
   constexpr int kind = IS_K ? CB_KIND_K : CB_KIND_V;
-  // Un-rotation table rows loaded one sub-tile ahead (keys only).
-  constexpr int TG = IS_K ? G : 1;
+  constexpr int TG = IS_K ? G : 1;   // un-rotation table values per lane (keys only)
+  constexpr int NGRP = RT / 4;       // row-tile groups: tiles {2h, 2h+1} and partners {2h, 2h+1} + RT/2
+  constexpr int NSTEP = 4 * KS;      // (row tile, k-step) steps of one group
+  constexpr int SUBT = 16 * CT;      // tokens per wave sub-tile (CT column tiles share each W fragment)
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -530,133 +537,162 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, cons
   const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
 
   const int n = wk.tok_hi - wk.tok_lo;
-  const int nsub = (n + kSubTokens - 1) / kSubTokens;
+  const int nsub = (n + SUBT - 1) / SUBT;
   int errbits = 0;
-  // Source and target rows of this lane's token in sub-tile `sub` (-1: skip).
-  // The index loads are issued two sub-tiles ahead (fetch) and resolved one
-  // sub-tile ahead (finish); tokens past the range re-read the range's last
-  // token and are masked.
-  auto token_of = [&](int sub) { return wk.tok_lo + min(sub * kSubTokens + col, n - 1); };
+  // Source and target rows of this lane's tokens in sub-tile `sub` (-1: skip).
+  // Index loads are issued four sub-tiles (of this wave) ahead and resolved
+  // two ahead, when that sub-tile's source dims are requested; tokens past
+  // the range re-read the range's last token and are masked.
   const CB_GLOBAL uint32_t* spare = reinterpret_cast<const CB_GLOBAL uint32_t*>(as_global(a.sink));
-  auto fetch_rows = [&](int sub, uint2& fs, uint2& fd) {
-    fs = row_fetch(a.src, token_of(sub), spare);
-    fd = row_fetch(a.tgt, token_of(sub), spare);
+  auto index_of = [&](int sub, int ct) { return sub * SUBT + ct * 16 + col; };
+  auto token_of = [&](int sub, int ct) { return wk.tok_lo + min(index_of(sub, ct), n - 1); };
+  auto fetch_rows = [&](int sub, uint2 (&fs)[CT], uint2 (&fd)[CT]) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      fs[ct] = row_fetch(a.src, token_of(sub, ct), spare);
+      fd[ct] = row_fetch(a.tgt, token_of(sub, ct), spare);
+    }
   };
-  auto finish_rows = [&](int sub, uint2 fs, uint2 fd, int32_t& sr, int32_t& tr) {
-    const int t = token_of(sub);
-    const int64_t s = row_finish(a.src, t, fs);
-    const int64_t d = row_finish(a.tgt, t, fd);
-    const bool live = sub * kSubTokens + col < n;
-    const bool sok = s >= 0 && s < a.src.rows;
-    const bool dok = d >= 0 && d < a.tgt.rows;
-    errbits |= live ? (sok ? 0 : 1) | (dok ? 0 : 2) : 0;
-    sr = live && sok ? static_cast<int32_t>(s) : -1;
-    tr = live && dok ? static_cast<int32_t>(d) : -1;
+  auto finish_rows = [&](int sub, const uint2 (&fs)[CT], const uint2 (&fd)[CT], int32_t (&sr)[CT],
+                         int32_t (&tr)[CT]) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int t = token_of(sub, ct);
+      const int64_t s = row_finish(a.src, t, fs[ct]);
+      const int64_t d = row_finish(a.tgt, t, fd[ct]);
+      const bool live = index_of(sub, ct) < n;
+      const bool sok = s >= 0 && s < a.src.rows;
+      const bool dok = d >= 0 && d < a.tgt.rows;
+      errbits |= live ? (sok ? 0 : 1) | (dok ? 0 : 2) : 0;
+      sr[ct] = live && sok ? static_cast<int32_t>(s) : -1;
+      tr[ct] = live && dok ? static_cast<int32_t>(d) : -1;
+    }
   };
 
-  uint4 xr[2][C::RUN_U4];           // raw source dims of the next sub-tile: [half][16 B]
-  float uc[TG], us[TG];             // its un-rotation table values
-  int32_t row_next = -1;
-  auto prefetch = [&](int sub, int32_t srow) {
-    const int i = sub * kSubTokens + col;
-    row_next = srow;
-    {
+  // Source dims and un-rotation tables of the next two sub-tiles (stage = k & 1
+  // for this wave's k-th sub-tile).
+  uint4 xr[2][CT][2][C::RUN_U4];
+  float uc[2][CT][TG], us[2][CT][TG];
+  bool live_x[2][CT];
+  auto prefetch = [&](int st, int sub, const int32_t (&srow)[CT]) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      live_x[st][ct] = srow[ct] >= 0;
       // Rows without a source read row 0 (always valid) and are zeroed on use.
-      const int64_t r = srow >= 0 ? srow : 0;
+      const int64_t r = srow[ct] >= 0 ? srow[ct] : 0;
       gcptr p = sbase + r * a.src.row_stride_b + g * G * C::BYTES;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int u = 0; u < C::RUN_U4; ++u)
-          xr[h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
+          xr[st][ct][h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
+      if constexpr (IS_K) {
+        const int64_t off = static_cast<int64_t>(a.position_start + token_of(sub, ct)) * HALF;
+        load_tab<G>(ucos + off, g, uc[st][ct]);
+        load_tab<G>(usin + off, g, us[st][ct]);
+      }
     }
-    if constexpr (IS_K) {
-      const int64_t off = static_cast<int64_t>(a.position_start + wk.tok_lo + min(i, n - 1)) * HALF;
-      load_tab<G>(ucos + off, g, uc);
-      load_tab<G>(usin + off, g, us);
+  };
+  auto dummy_stores = [&]() {
+    float zero[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) zero[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NJ * NGRP * CT; ++i) {
+      store_elems<IO, 8>(sink, zero);
+      store_elems<IO, 8>(sink + HALF * C::BYTES, zero);
     }
   };
 
-  // Segment start: the unit's W and bias, the first rows and the first
-  // sub-tile are loaded before waiting for the workgroup's previous segment
-  // to release LDS, so their latency overlaps that segment's tail.
-  int sub = wave;
-  int32_t sr_a, tr_a, sr_b, tr_b;
-  uint2 fs, fd;
-  fetch_rows(sub, fs, fd);
-  constexpr int WTOT = NJ * C::W_U4;
-  constexpr int WPER = (WTOT + kStreamThreads - 1) / kStreamThreads;
-  static_assert(NJ * D <= kStreamThreads, "staging split");
+  // Sub-tiles are claimed in order by each wave: its first four statically
+  // (wave + 8k), the rest from a workgroup counter in LDS as the wave moves
+  // along, so faster waves take more of the segment and all waves finish
+  // within about one sub-tile of each other. Claims past the segment end are
+  // dead (masked, no MFMAs). A claim is made when its index loads are issued,
+  // four sub-tiles ahead of its multiply.
+  constexpr int SW = kStreamWaves;
+  constexpr int kStatic = 4 * SW;
+  int c0 = wave, c1 = wave + SW, c2 = wave + 2 * SW, c3 = wave + 3 * SW;  // claim pipeline
+  auto claim = [&]() {  // one claim per wave, broadcast to all lanes
+    int v = 0;
+    if (lane == 0) v = atomicAdd(lds_next, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+
+  // Segment start: the unit's W and bias, the first rows and the first two
+  // sub-tiles are requested before waiting for the workgroup's previous
+  // segment to release LDS, so their latency overlaps that segment's tail.
+  int32_t sr0[CT], sr1[CT], tr_a[CT], tr_b[CT];
+  uint2 fs_a[CT], fd_a[CT], fs_b[CT], fd_b[CT];  // index loads of sub-tiles +2 and +3 ahead
+  fetch_rows(c0, fs_a, fd_a);
+  fetch_rows(c1, fs_b, fd_b);
+  constexpr int WPER = NJ * C::W_U4 / kStreamThreads;
+  static_assert(NJ * C::W_U4 % kStreamThreads == 0 && NJ * D <= kStreamThreads, "staging split");
   uint4 wreg[WPER];
   {
     gcptr wsrc = as_global(a.w + static_cast<size_t>(wk.job) * C::W_U4);
 #pragma unroll
-    for (int i = 0; i < WPER; ++i) {
-      const int e = i * kStreamThreads + threadIdx.x;
-      wreg[i] = (WTOT % kStreamThreads == 0 || e < WTOT) ? gload<uint4>(wsrc + e * 16) : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < WPER; ++i) wreg[i] = gload<uint4>(wsrc + (i * kStreamThreads + threadIdx.x) * 16);
   }
   const float breg = threadIdx.x < NJ * D ? a.bias[static_cast<size_t>(wk.job) * D + threadIdx.x] : 0.f;
-  finish_rows(sub, fs, fd, sr_a, tr_a);
-  prefetch(sub, sr_a);
-  fetch_rows(sub + kStreamWaves, fs, fd);
-  __syncthreads();  // the previous segment no longer reads LDS
+  finish_rows(c0, fs_a, fd_a, sr0, tr_a);
+  finish_rows(c1, fs_b, fd_b, sr1, tr_b);
+  // Outstanding at loop entry, oldest first, as after any iteration:
+  // x(k), rows(k+2), stores, x(k+1), rows(k+3), stores.
+  prefetch(0, c0, sr0);
+  fetch_rows(c2, fs_a, fd_a);
+  __syncthreads();  // the previous segment no longer reads LDS (nor claims)
 #pragma unroll
-  for (int i = 0; i < WPER; ++i) {
-    const int e = i * kStreamThreads + threadIdx.x;
-    if (WTOT % kStreamThreads == 0 || e < WTOT) lds_w[e] = wreg[i];
-  }
+  for (int i = 0; i < WPER; ++i) lds_w[i * kStreamThreads + threadIdx.x] = wreg[i];
   if (threadIdx.x < NJ * D) lds_bias[threadIdx.x] = breg;
-  __syncthreads();  // W and bias staged
-  // Enter the loop with the memory operations of one iteration outstanding in
-  // the same order (x and tables, row indices, NJ row stores; the stores go to
-  // the sink), so the compiler's waits inside the loop only cover the loads
-  // they need instead of draining every outstanding operation.
-  {
-    float zero[G];
-#pragma unroll
-    for (int e = 0; e < G; ++e) zero[e] = 0.f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      store_elems<IO, G>(sink + (g * G) * C::BYTES, zero);
-      store_elems<IO, G>(sink + (HALF + g * G) * C::BYTES, zero);
-    }
-  }
-  for (; sub < nsub; sub += kStreamWaves) {
+  if (threadIdx.x == 0) *lds_next = kStatic;
+  dummy_stores();
+  prefetch(1, c1, sr1);
+  fetch_rows(c3, fs_b, fd_b);
+  __syncthreads();  // W, bias and claim counter ready
+  dummy_stores();
+
+  // One sub-tile of this wave; the prefetch stage is a compile-time constant
+  // (register arrays indexed at run time would be placed in scratch memory).
+  // Sub-tiles past the segment run masked (rows -1) and skip their MFMAs.
+  auto body = [&](auto stage, int sub) {
+    constexpr int st = decltype(stage)::value;
+    const bool alive = sub < nsub;
     // W fragments are re-read from LDS every sub-tile: keep the compiler from
-    // hoisting all of them into registers.
+    // hoisting them into registers.
     asm volatile("" ::: "memory");
-    const int i = sub * kSubTokens + col;
-    const int64_t trow = tr_a;
-    const bool have = row_next >= 0;
+    int32_t trow[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) trow[ct] = tr_a[ct];
 
     // Un-rotate (keys) and split the current sub-tile into B fragments.
-    bf16x8 bx[KS][XT];
-    float tc[SHARED ? G : 1], ts[SHARED ? G : 1];
-    {
+    bf16x8 bx[CT][KS][XT];
+    float tc[CT][SHARED ? G : 1], ts[CT][SHARED ? G : 1];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
       float x1[G], x2[G];
 #pragma unroll
       for (int u = 0; u < C::RUN_U4; ++u) {
-        unpack16<IO>(xr[0][u], x1 + u * C::E16);
-        unpack16<IO>(xr[1][u], x2 + u * C::E16);
+        unpack16<IO>(xr[st][ct][0][u], x1 + u * C::E16);
+        unpack16<IO>(xr[st][ct][1][u], x2 + u * C::E16);
       }
       if constexpr (IS_K) {
 #pragma unroll
         for (int e = 0; e < G; ++e) {
-          const float k1 = x1[e] * uc[e] + x2[e] * us[e];
-          const float k2 = x2[e] * uc[e] - x1[e] * us[e];
+          const float k1 = x1[e] * uc[st][ct][e] + x2[e] * us[st][ct][e];
+          const float k2 = x2[e] * uc[st][ct][e] - x1[e] * us[st][ct][e];
           x1[e] = k1;
           x2[e] = k2;
         }
         if constexpr (SHARED) {
 #pragma unroll
           for (int e = 0; e < G; ++e) {
-            tc[e] = uc[e];
-            ts[e] = us[e];
+            tc[ct][e] = uc[st][ct][e];
+            ts[ct][e] = us[st][ct][e];
           }
         }
       }
-      if (!have) {
+      if (!live_x[st][ct]) {
 #pragma unroll
         for (int e = 0; e < G; ++e) x1[e] = x2[e] = 0.f;
       }
@@ -667,79 +703,119 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, cons
         split_terms<XT, 8>(src, tw);
 #pragma unroll
         for (int x = 0; x < XT; ++x)
-          bx[ks][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
+          bx[ct][ks][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
       }
     }
-    // Next sub-tile's source rows and tables load while this one is
-    // multiplied; the index loads of the sub-tile after it are issued too.
-    finish_rows(sub + kStreamWaves, fs, fd, sr_b, tr_b);
-    prefetch(sub + kStreamWaves, sr_b);
-    tr_a = tr_b;
-    fetch_rows(sub + 2 * kStreamWaves, fs, fd);
+    // The sub-tile two ahead: resolve its rows, request its source dims into
+    // the stage just consumed, and claim the sub-tile four ahead and issue
+    // its index loads.
+    {
+      int32_t sr2[CT], tr2[CT];
+      finish_rows(c2, fs_a, fd_a, sr2, tr2);
+      prefetch(st, c2, sr2);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        fs_a[ct] = fs_b[ct];
+        fd_a[ct] = fd_b[ct];
+      }
+      const int c4 = claim();
+      fetch_rows(c4, fs_b, fd_b);
+      c0 = c1;
+      c1 = c2;
+      c2 = c3;
+      c3 = c4;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        tr_a[ct] = tr_b[ct];
+        tr_b[ct] = tr2[ct];
+      }
+    }
 
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const uint4* wj = lds_w + j * C::W_U4;
-      f32x4 acc[RT];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const float* b = lds_bias + j * D + gen_out_dim(D, rt, 4 * g);
-        acc[rt] = f32x4{b[0], b[1], b[2], b[3]};
-      }
-      // W fragments of row tile rt+1 are read from LDS while rt multiplies.
-      bf16x8 aw[2][KS][NTW];
-      auto read_w = [&](int rt, bf16x8 (&dst)[KS][NTW]) {
+      for (int hg = 0; hg < NGRP; ++hg) {
+        // Row tiles of this group: 2hg, 2hg+1 and their partners.
+        auto tile = [&](int q) { return 2 * hg + (q & 1) + (q >> 1) * (RT / 2); };
+        f32x4 acc[4][CT];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+        for (int q = 0; q < 4; ++q) {
+          const float* b = lds_bias + j * D + gen_out_dim(D, tile(q), 4 * g);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) acc[q][ct] = f32x4{b[0], b[1], b[2], b[3]};
+        }
+        // W fragments flow through a three-slot ring, read two steps ahead;
+        // each fragment feeds the CT column tiles.
+        bf16x8 ring[3][NTW];
+        auto read_w = [&](int t, bf16x8 (&dst)[NTW]) {
+          const int rt = tile(t / KS), ks = t % KS;
 #pragma unroll
           for (int w = 0; w < NTW; ++w)
-            dst[ks][w] = __builtin_bit_cast(bf16x8, wj[((rt * KS + ks) * NTW + w) * kWave + lane]);
-      };
-      read_w(0, aw[0]);
+            dst[w] = __builtin_bit_cast(bf16x8, wj[((rt * KS + ks) * NTW + w) * kWave + lane]);
+        };
+        if (alive) {
+          read_w(0, ring[0]);
+          read_w(1, ring[1]);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        if (rt + 1 < RT) read_w(rt + 1, aw[(rt + 1) & 1]);
-        // Keep the reads above this row tile's MFMAs so they stay in flight.
-        __builtin_amdgcn_sched_barrier(0);
+          for (int t = 0; t < NSTEP; ++t) {
+            if (t + 2 < NSTEP) read_w(t + 2, ring[(t + 2) % 3]);
+            __builtin_amdgcn_sched_barrier(0);
+            const int ks = t % KS, q = t / KS;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          for_products<XT, NTW>([&](int ii, int jj) { acc[rt] = mfma(aw[rt & 1][ks][jj], bx[ks][ii], acc[rt]); });
-        __builtin_amdgcn_sched_barrier(0);
-      }
-
-      // Epilogue: target RoPE (keys), cast, scatter.
-      {
-        float o1[G], o2[G];
-#pragma unroll
-        for (int rt = 0; rt < RT / 2; ++rt)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            o1[4 * rt + q] = acc[rt][q];
-            o2[4 * rt + q] = acc[rt + RT / 2][q];
-          }
-        if constexpr (IS_K) {
-          float cbuf[G], sbuf[G];
-          const float* c = tc;
-          const float* s = ts;
-          if constexpr (!SHARED) {
-            const int64_t off = static_cast<int64_t>(a.position_start + wk.tok_lo + min(i, n - 1)) * HALF;
-            load_tab<G>(rcos + off, g, cbuf);
-            load_tab<G>(rsin + off, g, sbuf);
-            c = cbuf;
-            s = sbuf;
-          }
-#pragma unroll
-          for (int e = 0; e < G; ++e) {
-            const float y1 = o1[e], y2 = o2[e];
-            o1[e] = y1 * c[e] - y2 * s[e];
-            o2[e] = y2 * c[e] + y1 * s[e];
+            for (int ct = 0; ct < CT; ++ct)
+              for_products<XT, NTW>(
+                  [&](int ii, int jj) { acc[q][ct] = mfma(ring[t % 3][jj], bx[ct][ks][ii], acc[q][ct]); });
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
-        gptr p = trow >= 0 ? tbase[j] + trow * a.tgt.row_stride_b : sink;
-        store_elems<IO, G>(p + (g * G) * C::BYTES, o1);
-        store_elems<IO, G>(p + (HALF + g * G) * C::BYTES, o2);
+        // Epilogue of the group: 8 output dims of each half, target RoPE
+        // (keys), cast, 16-byte stores.
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          float o1[8], o2[8];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            o1[q] = acc[0][ct][q];
+            o1[4 + q] = acc[1][ct][q];
+            o2[q] = acc[2][ct][q];
+            o2[4 + q] = acc[3][ct][q];
+          }
+          if constexpr (IS_K) {
+            float cbuf[8], sbuf[8];
+            if constexpr (SHARED) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                cbuf[e] = tc[ct][8 * hg + e];
+                sbuf[e] = ts[ct][8 * hg + e];
+              }
+            } else {
+              const int64_t off = static_cast<int64_t>(a.position_start + token_of(sub, ct)) * HALF;
+#pragma unroll
+              for (int u = 0; u < 2; ++u) {
+                const float4 cv = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off + (2 * hg + u) * 16 + g * 4);
+                const float4 sv = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off + (2 * hg + u) * 16 + g * 4);
+                cbuf[4 * u] = cv.x; cbuf[4 * u + 1] = cv.y; cbuf[4 * u + 2] = cv.z; cbuf[4 * u + 3] = cv.w;
+                sbuf[4 * u] = sv.x; sbuf[4 * u + 1] = sv.y; sbuf[4 * u + 2] = sv.z; sbuf[4 * u + 3] = sv.w;
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float y1 = o1[e], y2 = o2[e];
+              o1[e] = y1 * cbuf[e] - y2 * sbuf[e];
+              o2[e] = y2 * cbuf[e] + y1 * sbuf[e];
+            }
+          }
+          gptr p = trow[ct] >= 0 ? tbase[j] + static_cast<int64_t>(trow[ct]) * a.tgt.row_stride_b : sink;
+          store_elems<IO, 8>(p + (g * G + 8 * hg) * C::BYTES, o1);
+          store_elems<IO, 8>(p + (HALF + g * G + 8 * hg) * C::BYTES, o2);
+        }
       }
     }
+  };
+  while (c0 < nsub) {
+    body(std::integral_constant<int, 0>{}, c0);
+    body(std::integral_constant<int, 1>{}, c0);
   }
   if (errbits) atomicOr(a.err, errbits);
 }
@@ -748,6 +824,7 @@ template <int D, typename IO>
 __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapArgs a) {
   __shared__ uint4 lds_w[kUnitJobs * Gm<D, IO>::W_U4];
   __shared__ float lds_bias[kUnitJobs * D];
+  __shared__ int lds_next;  // next sub-tile to claim in the current segment
   const int per = a.num_blocks >> 3;
   const int r = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
   Pos cur{a.blk_unit[r], a.blk_sub[r]};
@@ -765,15 +842,15 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
       const bool two = wk.njobs == 2;
       if ((meta.y & 0xff) == CB_KIND_K) {
         if (meta.z & kJobSharedTables) {
-          if (two) stream_run<D, IO, true, true, 2>(a, lds_w, lds_bias, wk);
-          else stream_run<D, IO, true, true, 1>(a, lds_w, lds_bias, wk);
+          if (two) stream_run<D, IO, true, true, 2, 1>(a, lds_w, lds_bias, &lds_next, wk);
+          else stream_run<D, IO, true, true, 1, 1>(a, lds_w, lds_bias, &lds_next, wk);
         } else {
-          if (two) stream_run<D, IO, true, false, 2>(a, lds_w, lds_bias, wk);
-          else stream_run<D, IO, true, false, 1>(a, lds_w, lds_bias, wk);
+          if (two) stream_run<D, IO, true, false, 2, 1>(a, lds_w, lds_bias, &lds_next, wk);
+          else stream_run<D, IO, true, false, 1, 1>(a, lds_w, lds_bias, &lds_next, wk);
         }
       } else {
-        if (two) stream_run<D, IO, false, false, 2>(a, lds_w, lds_bias, wk);
-        else stream_run<D, IO, false, false, 1>(a, lds_w, lds_bias, wk);
+        if (two) stream_run<D, IO, false, false, 2, 2>(a, lds_w, lds_bias, &lds_next, wk);
+        else stream_run<D, IO, false, false, 1, 2>(a, lds_w, lds_bias, &lds_next, wk);
       }
     }
     cur = Pos{cur.unit + 1, 0};

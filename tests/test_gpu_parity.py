@@ -124,9 +124,14 @@ def _check_pools(h, expected, mapped, tgt_slots):
             assert torch.equal(got[:, l, :f], want_untouched)
 
 
-@pytest.mark.parametrize("name,tokens", [("tp4", 512), ("full", 256), ("gemma", 1200)])
-def test_fused_pool_install_matches_oracle(name, tokens):
+@pytest.mark.parametrize("name,tokens,layers,tpw", [("tp4", 512, None, 0), ("full", 256, None, 0),
+                                                   ("gemma", 1200, None, 0), ("tp4", 2048, 6, 2048)])
+def test_fused_pool_install_matches_oracle(name, tokens, layers, tpw):
+    """tpw: cap on tokens per workgroup, forcing many workgroups with long segments."""
+    print(f"fused install {name} tokens={tokens} layers={layers} tpw={tpw}", flush=True)
     sh = synthetic.shape(name, tokens=tokens)
+    if layers is not None:
+        sh.target_layers = layers
     if name == "gemma":
         sh.target_layers = 12  # keeps global layers 5 and 11 and their local neighbours
         sh.windows = sh.windows[:12]
@@ -137,7 +142,7 @@ def test_fused_pool_install_matches_oracle(name, tokens):
     h.target_pool.k_data.copy_(torch.randn_like(h.target_pool.k_data, dtype=torch.float32))
     h.target_pool.v_data.copy_(torch.randn_like(h.target_pool.v_data, dtype=torch.float32))
     before = _cpu_pool(h.target_pool)
-    h.run()
+    h.run(tokens_per_workgroup=tpw)
     assert h.mapper.plan.read_errors() == 0
     mapped, tgt_slots = _oracle_install(h, before)
     _check_pools(h, before, mapped, tgt_slots)
