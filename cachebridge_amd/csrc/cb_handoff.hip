@@ -760,7 +760,6 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
 #pragma unroll
           for (int t = 0; t < NSTEP; ++t) {
             if (t + 2 < NSTEP) read_w(t + 2, ring[(t + 2) % 3]);
-            __builtin_amdgcn_sched_barrier(0);
             const int ks = t % KS, q = t / KS;
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct)
