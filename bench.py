@@ -40,6 +40,11 @@ WORKLOADS = {
            "65536-page target pool with a shuffled free list",
     "full": "Qwen3-14B->32B whole model on one GPU: source 40x8 -> target 64x8 KV heads, head_dim "
             "128, 4096 tokens, bf16, page 16, 8192-page target pool",
+    "full32k": "Qwen3-14B->32B whole model, long history: source 40x8 -> target 64x8 KV heads, "
+               "head_dim 128, 32768 tokens, bf16, page 16, 4096-page target pool",
+    "gemma": "Gemma-3-style target: source 40x8 -> target 62x16 KV heads (10 global layers keep all "
+             "8192 tokens, 52 sliding-window layers keep the last 1023), head map h_src = h // 2, "
+             "theta 1e4 local / 1e6 global, head_dim 128, bf16, page 16",
 }
 
 
@@ -166,7 +171,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="tp4", choices=sorted(WORKLOADS))
-    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--tokens", type=int, default=None,
+                    help="history length (default: the workload's own)")
     ap.add_argument("--tokens-per-workgroup", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
@@ -225,7 +231,7 @@ def main() -> int:
     }
     del h
     torch.cuda.empty_cache()
-    if not args.no_north_star and args.workload != "full":
+    if not args.no_north_star and args.workload == "tp4":
         ns = synthetic.shape("full", tokens=4096)
         hn = synthetic.make_handoff(ns)
         wall_n, kms_n, _ = time_handoff(hn, max(20, args.steps // 4), args.warmup)
