@@ -94,6 +94,17 @@ class CbRequest(ctypes.Structure):
     ]
 
 
+class CbSpan(ctypes.Structure):
+    _fields_ = [
+        ("source_offset", _i64),
+        ("target_offset", _i64),
+        ("num_tokens", _i32),
+        ("position_start", _i32),
+        ("prefix_length", _i32),
+        ("reserved", _i32),
+    ]
+
+
 class CbPlanInfo(ctypes.Structure):
     _fields_ = [
         ("head_dim", _i32),
@@ -118,6 +129,13 @@ SIGNATURES = {
     "cb_plan_destroy": (None, [_c_void_p]),
     "cb_plan_get_info": (ctypes.c_int, [_c_void_p, ctypes.POINTER(CbPlanInfo)]),
     "cb_map_install": (ctypes.c_int, [_c_void_p, ctypes.POINTER(CbRequest), _c_void_p]),
+    "cb_batch_workspace_bytes": (ctypes.c_int, [_c_void_p, ctypes.POINTER(CbSpan), _i32,
+                                                ctypes.POINTER(_i64)]),
+    "cb_map_install_batch": (
+        ctypes.c_int,
+        [_c_void_p, ctypes.POINTER(CbRows), ctypes.POINTER(CbRows), ctypes.POINTER(CbSpan), _i32,
+         _c_void_p, _i64, _c_void_p],
+    ),
     "cb_copy_rows": (
         ctypes.c_int,
         [ctypes.POINTER(CbRows), ctypes.POINTER(CbRows), _i32, _i32, _i32, _i32, _c_void_p, _c_void_p],

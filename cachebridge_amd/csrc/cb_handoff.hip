@@ -335,6 +335,10 @@ struct MapArgs {
   int32_t blk_sub[kMaxStreamBlocks + 1];
   int32_t* err;
   void* sink;  // scratch destination of stores without a target row
+  // Batched launches: position of every token (tokens then index resolved
+  // rows: src/tgt are int32 row vectors over the same token space). Null for
+  // one request, whose token t sits at position_start + t.
+  const int32_t* pos;
 };
 
 // Job flag (meta.z): un-rotation uses the rotation table (same theta, unit norm).
@@ -398,6 +402,11 @@ __host__ __device__ inline Pos cost_to_pos(const MapArgs& a, int64_t P) {
   }
   const int64_t w = a.unit_cost_prefix[lo + 1] - a.unit_cost_prefix[lo];
   return Pos{lo, static_cast<int>((q - (a.unit_cost_prefix[lo] - base) * ns) / w)};
+}
+
+// Position of token t of the launch (see MapArgs::pos).
+__device__ inline int position_of(const MapArgs& a, int t) {
+  return a.pos ? reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(a.pos))[t] : a.position_start + t;
 }
 
 __host__ __device__ inline int class_of_unit(const MapArgs& a, int u) {
@@ -489,7 +498,7 @@ struct Gm {
   static constexpr int W_U4 = RT * KS * NTW * kWave;
 };
 
-template <int D, typename IO, bool IS_K, bool SHARED, int NJ, int CT>
+template <int D, typename IO, bool IS_K, bool SHARED, int NJ, int CT, bool POS>
 __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int* lds_next, const Work& wk) {
   // Separately rounded products and sums (as the reference's torch ops), so
   // every instantiation rounds identically: a job's rows are bit-identical
@@ -505,6 +514,9 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   constexpr int NGRP = RT / 4;       // row-tile groups: tiles {2h, 2h+1} and partners {2h, 2h+1} + RT/2
   constexpr int NSTEP = 4 * KS;      // (row tile, k-step) steps of one group
   constexpr int SUBT = 16 * CT;      // tokens per wave sub-tile (CT column tiles share each W fragment)
+  // Keys of a batched launch read each token's position from a.pos (issued
+  // with the index words); otherwise token t sits at position_start + t.
+  constexpr bool PV = POS && IS_K;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -546,18 +558,20 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   const CB_GLOBAL uint32_t* spare = reinterpret_cast<const CB_GLOBAL uint32_t*>(as_global(a.sink));
   auto index_of = [&](int sub, int ct) { return sub * SUBT + ct * 16 + col; };
   auto token_of = [&](int sub, int ct) { return wk.tok_lo + min(index_of(sub, ct), n - 1); };
-  auto fetch_rows = [&](int sub, uint2 (&fs)[CT], uint2 (&fd)[CT]) {
+  auto fetch_rows = [&](int sub, uint2 (&fs)[CT], uint2 (&fd)[CT], int32_t (&fp)[CT]) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       fs[ct] = row_fetch(a.src, token_of(sub, ct), spare);
       fd[ct] = row_fetch(a.tgt, token_of(sub, ct), spare);
+      if constexpr (PV) fp[ct] = reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(a.pos))[token_of(sub, ct)];
     }
   };
-  auto finish_rows = [&](int sub, const uint2 (&fs)[CT], const uint2 (&fd)[CT], int32_t (&sr)[CT],
-                         int32_t (&tr)[CT]) {
+  auto finish_rows = [&](int sub, const uint2 (&fs)[CT], const uint2 (&fd)[CT], const int32_t (&fp)[CT],
+                         int32_t (&sr)[CT], int32_t (&tr)[CT], int32_t (&pr)[CT]) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       const int t = token_of(sub, ct);
+      pr[ct] = PV ? fp[ct] : a.position_start + t;
       const int64_t s = row_finish(a.src, t, fs[ct]);
       const int64_t d = row_finish(a.tgt, t, fd[ct]);
       const bool live = index_of(sub, ct) < n;
@@ -574,7 +588,7 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   uint4 xr[2][CT][2][C::RUN_U4];
   float uc[2][CT][TG], us[2][CT][TG];
   bool live_x[2][CT];
-  auto prefetch = [&](int st, int sub, const int32_t (&srow)[CT]) {
+  auto prefetch = [&](int st, int sub, const int32_t (&srow)[CT], const int32_t (&prow)[CT]) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       live_x[st][ct] = srow[ct] >= 0;
@@ -587,7 +601,7 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
         for (int u = 0; u < C::RUN_U4; ++u)
           xr[st][ct][h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
       if constexpr (IS_K) {
-        const int64_t off = static_cast<int64_t>(a.position_start + token_of(sub, ct)) * HALF;
+        const int64_t off = static_cast<int64_t>(PV ? prow[ct] : a.position_start + token_of(sub, ct)) * HALF;
         load_tab<G>(ucos + off, g, uc[st][ct]);
         load_tab<G>(usin + off, g, us[st][ct]);
       }
@@ -622,10 +636,12 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   // Segment start: the unit's W and bias, the first rows and the first two
   // sub-tiles are requested before waiting for the workgroup's previous
   // segment to release LDS, so their latency overlaps that segment's tail.
-  int32_t sr0[CT], sr1[CT], tr_a[CT], tr_b[CT];
+  int32_t sr0[CT], sr1[CT], tr_a[CT], tr_b[CT], pr0[CT], pr1[CT];
+  int32_t pr_a[CT], pr_b[CT];                    // positions of the current and next sub-tile (batched keys)
   uint2 fs_a[CT], fd_a[CT], fs_b[CT], fd_b[CT];  // index loads of sub-tiles +2 and +3 ahead
-  fetch_rows(c0, fs_a, fd_a);
-  fetch_rows(c1, fs_b, fd_b);
+  int32_t fp_a[CT], fp_b[CT];                    // their position words (batched keys)
+  fetch_rows(c0, fs_a, fd_a, fp_a);
+  fetch_rows(c1, fs_b, fd_b, fp_b);
   constexpr int WPER = NJ * C::W_U4 / kStreamThreads;
   static_assert(NJ * C::W_U4 % kStreamThreads == 0 && NJ * D <= kStreamThreads, "staging split");
   uint4 wreg[WPER];
@@ -635,20 +651,25 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     for (int i = 0; i < WPER; ++i) wreg[i] = gload<uint4>(wsrc + (i * kStreamThreads + threadIdx.x) * 16);
   }
   const float breg = threadIdx.x < NJ * D ? a.bias[static_cast<size_t>(wk.job) * D + threadIdx.x] : 0.f;
-  finish_rows(c0, fs_a, fd_a, sr0, tr_a);
-  finish_rows(c1, fs_b, fd_b, sr1, tr_b);
+  finish_rows(c0, fs_a, fd_a, fp_a, sr0, tr_a, pr0);
+  finish_rows(c1, fs_b, fd_b, fp_b, sr1, tr_b, pr1);
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    pr_a[ct] = pr0[ct];
+    pr_b[ct] = pr1[ct];
+  }
   // Outstanding at loop entry, oldest first, as after any iteration:
   // x(k), rows(k+2), stores, x(k+1), rows(k+3), stores.
-  prefetch(0, c0, sr0);
-  fetch_rows(c2, fs_a, fd_a);
+  prefetch(0, c0, sr0, pr0);
+  fetch_rows(c2, fs_a, fd_a, fp_a);
   __syncthreads();  // the previous segment no longer reads LDS (nor claims)
 #pragma unroll
   for (int i = 0; i < WPER; ++i) lds_w[i * kStreamThreads + threadIdx.x] = wreg[i];
   if (threadIdx.x < NJ * D) lds_bias[threadIdx.x] = breg;
   if (threadIdx.x == 0) *lds_next = kStatic;
   dummy_stores();
-  prefetch(1, c1, sr1);
-  fetch_rows(c3, fs_b, fd_b);
+  prefetch(1, c1, sr1, pr1);
+  fetch_rows(c3, fs_b, fd_b, fp_b);
   __syncthreads();  // W, bias and claim counter ready
   dummy_stores();
 
@@ -661,9 +682,12 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     // W fragments are re-read from LDS every sub-tile: keep the compiler from
     // hoisting them into registers.
     asm volatile("" ::: "memory");
-    int32_t trow[CT];
+    int32_t trow[CT], prow[CT];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) trow[ct] = tr_a[ct];
+    for (int ct = 0; ct < CT; ++ct) {
+      trow[ct] = tr_a[ct];
+      prow[ct] = pr_a[ct];
+    }
 
     // Un-rotate (keys) and split the current sub-tile into B fragments.
     bf16x8 bx[CT][KS][XT];
@@ -710,16 +734,17 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     // the stage just consumed, and claim the sub-tile four ahead and issue
     // its index loads.
     {
-      int32_t sr2[CT], tr2[CT];
-      finish_rows(c2, fs_a, fd_a, sr2, tr2);
-      prefetch(st, c2, sr2);
+      int32_t sr2[CT], tr2[CT], pr2[CT];
+      finish_rows(c2, fs_a, fd_a, fp_a, sr2, tr2, pr2);
+      prefetch(st, c2, sr2, pr2);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         fs_a[ct] = fs_b[ct];
         fd_a[ct] = fd_b[ct];
+        fp_a[ct] = fp_b[ct];
       }
       const int c4 = claim();
-      fetch_rows(c4, fs_b, fd_b);
+      fetch_rows(c4, fs_b, fd_b, fp_b);
       c0 = c1;
       c1 = c2;
       c2 = c3;
@@ -728,6 +753,8 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       for (int ct = 0; ct < CT; ++ct) {
         tr_a[ct] = tr_b[ct];
         tr_b[ct] = tr2[ct];
+        pr_a[ct] = pr_b[ct];
+        pr_b[ct] = pr2[ct];
       }
     }
 
@@ -789,7 +816,7 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
                 sbuf[e] = ts[ct][8 * hg + e];
               }
             } else {
-              const int64_t off = static_cast<int64_t>(a.position_start + token_of(sub, ct)) * HALF;
+              const int64_t off = static_cast<int64_t>(PV ? prow[ct] : a.position_start + token_of(sub, ct)) * HALF;
 #pragma unroll
               for (int u = 0; u < 2; ++u) {
                 const float4 cv = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off + (2 * hg + u) * 16 + g * 4);
@@ -819,7 +846,7 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   if (errbits) atomicOr(a.err, errbits);
 }
 
-template <int D, typename IO>
+template <int D, typename IO, bool POS>
 __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapArgs a) {
   __shared__ uint4 lds_w[kUnitJobs * Gm<D, IO>::W_U4];
   __shared__ float lds_bias[kUnitJobs * D];
@@ -841,15 +868,15 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
       const bool two = wk.njobs == 2;
       if ((meta.y & 0xff) == CB_KIND_K) {
         if (meta.z & kJobSharedTables) {
-          if (two) stream_run<D, IO, true, true, 2, 1>(a, lds_w, lds_bias, &lds_next, wk);
-          else stream_run<D, IO, true, true, 1, 1>(a, lds_w, lds_bias, &lds_next, wk);
+          if (two) stream_run<D, IO, true, true, 2, 1, POS>(a, lds_w, lds_bias, &lds_next, wk);
+          else stream_run<D, IO, true, true, 1, 1, POS>(a, lds_w, lds_bias, &lds_next, wk);
         } else {
-          if (two) stream_run<D, IO, true, false, 2, 1>(a, lds_w, lds_bias, &lds_next, wk);
-          else stream_run<D, IO, true, false, 1, 1>(a, lds_w, lds_bias, &lds_next, wk);
+          if (two) stream_run<D, IO, true, false, 2, 1, POS>(a, lds_w, lds_bias, &lds_next, wk);
+          else stream_run<D, IO, true, false, 1, 1, POS>(a, lds_w, lds_bias, &lds_next, wk);
         }
       } else {
-        if (two) stream_run<D, IO, false, false, 2, 2>(a, lds_w, lds_bias, &lds_next, wk);
-        else stream_run<D, IO, false, false, 1, 2>(a, lds_w, lds_bias, &lds_next, wk);
+        if (two) stream_run<D, IO, false, false, 2, 2, POS>(a, lds_w, lds_bias, &lds_next, wk);
+        else stream_run<D, IO, false, false, 1, 2, POS>(a, lds_w, lds_bias, &lds_next, wk);
       }
     }
     cur = Pos{cur.unit + 1, 0};
@@ -951,7 +978,7 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
             unpack16<IO>(gload<uint4>(p + (HALF + g * G + u * C::E16) * T::BYTES), x2 + u * C::E16);
           }
           if constexpr (IS_K) {
-            const int64_t off = static_cast<int64_t>(a.position_start + tok[ct]) * HALF;
+            const int64_t off = static_cast<int64_t>(position_of(a, tok[ct])) * HALF;
             float c[G], s[G];
             load_tab<G>(ucos + off, g, c);
             load_tab<G>(usin + off, g, s);
@@ -1004,7 +1031,7 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
       float o1[G], o2[G];
       float c[G], s[G];
       if constexpr (IS_K) {
-        const int64_t off = static_cast<int64_t>(a.position_start + tok[ct]) * HALF;
+        const int64_t off = static_cast<int64_t>(position_of(a, tok[ct])) * HALF;
         load_tab<G>(rcos + off, g, c);
         load_tab<G>(rsin + off, g, s);
       }
@@ -1158,6 +1185,59 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(CopyArgs a) {
     const uint4 v = gload<uint4>(sbase + sr * a.src.row_stride_b + 16 * ch);
     gstore<uint4>(dbase + dr * a.dst.row_stride_b + 16 * ch, v);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Batched launches: every kept token of every request gets a slot in one
+// token space, class by class (class c's kept tokens of request r occupy
+// [vbase, vbase + count)). This kernel resolves each slot's source row,
+// target row and position once; the map kernel then reads them as int32 row
+// vectors, so a batch runs as one map launch.
+// ---------------------------------------------------------------------------
+
+constexpr int kBatchSpans = 32;  // requests per resolve launch (kernel arguments)
+
+struct BatchArgs {
+  DevRows src, tgt;
+  int32_t* src_row;
+  int32_t* tgt_row;
+  int32_t* pos;
+  int32_t nspans;
+  int32_t ncls;
+  int64_t src_off[kBatchSpans];
+  int64_t tgt_off[kBatchSpans];
+  int32_t pos0[kBatchSpans];
+  int32_t first[kMaxClasses][kBatchSpans];  // first kept token of the request in the class
+  int32_t count[kMaxClasses][kBatchSpans];
+  int32_t vbase[kMaxClasses][kBatchSpans];
+};
+static_assert(sizeof(BatchArgs) <= 4096, "kernel arguments must fit 4 KB");
+
+// Row of u = t + index_offset under R's index rule; -1 outside [0, rows).
+__device__ inline int32_t resolve_row(const DevRows& R, int64_t t) {
+  const int64_t u = t + R.index_offset;
+  int64_t row;
+  switch (R.index_kind) {
+    case CB_INDEX_IDENTITY: row = u; break;
+    case CB_INDEX_I32: row = reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(R.index))[u]; break;
+    case CB_INDEX_I64: row = reinterpret_cast<const CB_GLOBAL int64_t*>(as_global(R.index))[u]; break;
+    default: {
+      const int64_t ps = R.page_size;
+      row = static_cast<int64_t>(reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(R.index))[u / ps]) * ps + u % ps;
+    }
+  }
+  return row >= 0 && row < R.rows ? static_cast<int32_t>(row) : -1;
+}
+
+__global__ __launch_bounds__(256) void resolve_batch_kernel(BatchArgs b) {
+  const int c = blockIdx.y / b.nspans, r = blockIdx.y % b.nspans;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= b.count[c][r]) return;
+  const int t = b.first[c][r] + i;
+  const int v = b.vbase[c][r] + i;
+  b.pos[v] = b.pos0[r] + t;
+  b.src_row[v] = resolve_row(b.src, b.src_off[r] + t);
+  b.tgt_row[v] = resolve_row(b.tgt, b.tgt_off[r] + t);
 }
 
 }  // namespace
@@ -1430,6 +1510,206 @@ int default_chunk(const cb_plan* p, int n) {
   return static_cast<int>(std::min<int64_t>(chunk, 1 << 20));
 }
 
+// Geometry checks shared by single and batched launches (before anything is
+// enqueued).
+int check_sides(const cb_plan* p, const cb_rows& sr, const cb_rows& tr) {
+  const int D = p->info.head_dim;
+  if (sr.num_layers <= p->max_src_layer)
+    return fail(CB_EINVAL, "source has %d layers; the plan reads layer %d", sr.num_layers,
+                p->max_src_layer);
+  if (p->min_src_head < sr.head_offset || p->max_src_head >= sr.head_offset + sr.heads)
+    return fail(CB_EINVAL, "source rows hold heads [%d, %d); the plan reads heads %d..%d",
+                sr.head_offset, sr.head_offset + sr.heads, p->min_src_head, p->max_src_head);
+  if (tr.num_layers <= p->max_tgt_layer)
+    return fail(CB_EINVAL, "target has %d layers; the plan writes layer %d", tr.num_layers,
+                p->max_tgt_layer);
+  if (p->min_tgt_head < tr.head_offset || p->max_tgt_head >= tr.head_offset + tr.heads)
+    return fail(CB_EINVAL, "target rows hold heads [%d, %d); the plan writes heads %d..%d",
+                tr.head_offset, tr.head_offset + tr.heads, p->min_tgt_head, p->max_tgt_head);
+  if (static_cast<int64_t>(sr.heads) * D > sr.row_stride ||
+      static_cast<int64_t>(tr.heads) * D > tr.row_stride)
+    return fail(CB_EINVAL, "row_stride is smaller than heads * head_dim");
+  if (tr.index_kind == CB_INDEX_IDENTITY && sr.index_kind == CB_INDEX_IDENTITY &&
+      tr.k_base == sr.k_base && tr.k_base)
+    return fail(CB_EINVAL, "target aliases the source");
+  if (p->info.support == 1 && (sr.rows > INT32_MAX || tr.rows > INT32_MAX))
+    return fail(CB_EINVAL, "pools with more than 2^31 rows are not supported");
+  return CB_OK;
+}
+
+// Kept tokens of each window class for a request of n tokens at positions
+// position_start.. of a prefix of `prefix` tokens: [first[c], first[c] +
+// count[c]). A sliding class keeps the last min(prefix, window - 1) tokens of
+// the prefix (cb/architectures/gemma3.py:52); a full class keeps all.
+void class_ranges(const cb_plan* p, int64_t n, int64_t position_start, int64_t prefix,
+                  int64_t* first, int64_t* count) {
+  for (int c = 0; c < p->num_windows; ++c) {
+    int64_t first_pos = 0;
+    if (p->window_size[c] > 0) first_pos = prefix - std::min<int64_t>(prefix, p->window_size[c] - 1);
+    const int64_t f = std::max<int64_t>(0, first_pos - position_start);
+    count[c] = std::max<int64_t>(0, n - f);
+    first[c] = std::min<int64_t>(f, n);
+  }
+}
+
+// Enqueue the map kernel over class token ranges [first[c], first[c] +
+// count[c]) of the launch's token space. `a` carries the two sides (and, for
+// batches, the position vector); the plan fields are filled in here.
+// tokens_per_workgroup > 0 caps the unit-tokens per workgroup.
+int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t* count,
+               int tokens_per_workgroup, int default_tokens, hipStream_t s) {
+  const int D = p->info.head_dim;
+  const bool ws = p->info.support == 1;
+  const int unit = ws ? kSubTokens : kGenSubTokens;
+  int chunk = tokens_per_workgroup > 0 ? tokens_per_workgroup : default_tokens;
+  if (tokens_per_workgroup < 0 || chunk < unit || chunk % unit)
+    return fail(CB_EINVAL, "tokens_per_workgroup must be a positive multiple of %d", unit);
+  a.w = static_cast<const uint4*>(p->d_w);
+  a.bias = p->d_bias;
+  a.jobs = p->d_jobs;
+  a.pairs = p->d_pairs;
+  a.unit_job = p->d_unit_job;
+  a.unit_njobs = p->d_unit_njobs;
+  a.unit_group = p->d_unit_group;
+  a.group_unit_start = p->d_group_unit_start;
+  a.group_unit_count = p->d_group_unit_count;
+  a.cos_tab = p->d_cos;
+  a.sin_tab = p->d_sin;
+  a.ucos_tab = p->d_ucos;
+  a.usin_tab = p->d_usin;
+  a.theta_stride = static_cast<int64_t>(p->info.table_positions) * (D / 2);
+  a.support = p->info.support;
+  a.chunk = chunk;
+  a.err = p->d_err;
+  a.sink = p->d_sink;
+  int64_t items = 0, n_total = 0;
+  a.ncls = p->num_windows;
+  for (int c = 0; c < p->num_windows; ++c) {
+    if (first[c] + count[c] > INT32_MAX) return fail(CB_EINVAL, "launch too large");
+    const int64_t nch = (count[c] + chunk - 1) / chunk;
+    a.cls_unit_begin[c] = p->cls_unit_begin[c];
+    a.cls_tok_first[c] = static_cast<int32_t>(first[c]);
+    a.cls_tok_count[c] = static_cast<int32_t>(count[c]);
+    a.cls_nchunks[c] = static_cast<int32_t>(std::max<int64_t>(nch, 1));
+    a.cls_item_begin[c] = static_cast<int32_t>(items);
+    items += static_cast<int64_t>(p->cls_unit_end[c] - p->cls_unit_begin[c]) * nch;
+    n_total = std::max(n_total, first[c] + count[c]);
+  }
+  a.n_tokens = static_cast<int32_t>(n_total);
+  a.cls_item_begin[p->num_windows] = static_cast<int32_t>(items);
+  if (items == 0) return CB_OK;
+  if (items > (int64_t{1} << 30)) return fail(CB_EINVAL, "request too large for one launch");
+  a.total_items = static_cast<int32_t>(items);
+  a.padded_items = static_cast<int32_t>((items + 7) / 8 * 8);
+  int64_t grid_blocks = a.padded_items;
+  if (ws) {
+    // Cost line: class by class, unit weight x sub-tiles of the class.
+    int64_t cost = 0, unit_tokens = 0;
+    for (int c = 0; c < p->num_windows; ++c) {
+      const int64_t sub = (static_cast<int64_t>(a.cls_tok_count[c]) + kSubTokens - 1) / kSubTokens;
+      a.cls_unit_end[c] = p->cls_unit_end[c];
+      a.cls_subtiles[c] = static_cast<int32_t>(sub);
+      a.cls_cost_begin[c] = cost;
+      cost += (p->cls_unit_weight_end[c] - p->cls_unit_weight_begin[c]) * sub;
+      unit_tokens += static_cast<int64_t>(p->cls_unit_end[c] - p->cls_unit_begin[c]) * a.cls_tok_count[c];
+    }
+    a.cls_cost_begin[p->num_windows] = cost;
+    if (cost == 0) return CB_OK;
+    a.unit_cost_prefix = p->d_unit_cost_prefix;
+    a.num_units = p->num_units;
+    int64_t nb = p->num_cus;
+    if (tokens_per_workgroup > 0)  // cap on unit-tokens per workgroup
+      nb = std::min<int64_t>(nb, std::max<int64_t>(8, (unit_tokens + chunk - 1) / chunk));
+    a.num_blocks = static_cast<int32_t>(std::max<int64_t>(8, nb / 8 * 8));
+    grid_blocks = a.num_blocks;
+    MapArgs host = a;  // cost_to_pos reads the prefix through the args
+    host.unit_cost_prefix = p->h_unit_cost_prefix.data();
+    for (int r = 0; r <= a.num_blocks; ++r) {
+      const Pos q = cost_to_pos(host, cost * r / a.num_blocks);
+      a.blk_unit[r] = q.unit;
+      a.blk_sub[r] = q.sub;
+    }
+  }
+  const dim3 grid(static_cast<unsigned>(grid_blocks)), block(ws ? kStreamThreads : kThreads);
+  if (ws) {
+    const bool pv = a.pos != nullptr;
+    if (D == 128 && p->ntw == 2) {
+      if (pv) hipLaunchKernelGGL((map_install_stream_kernel<128, uint16_t, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((map_install_stream_kernel<128, uint16_t, false>), grid, block, 0, s, a);
+    } else if (D == 64 && p->ntw == 2) {
+      if (pv) hipLaunchKernelGGL((map_install_stream_kernel<64, uint16_t, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((map_install_stream_kernel<64, uint16_t, false>), grid, block, 0, s, a);
+    } else {
+      if (pv) hipLaunchKernelGGL((map_install_stream_kernel<64, float, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((map_install_stream_kernel<64, float, false>), grid, block, 0, s, a);
+    }
+  } else {
+    if (D == 128 && p->ntw == 2)
+      hipLaunchKernelGGL((map_install_gen_kernel<128, uint16_t>), grid, block, 0, s, a);
+    else if (D == 64 && p->ntw == 2)
+      hipLaunchKernelGGL((map_install_gen_kernel<64, uint16_t>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((map_install_gen_kernel<64, float>), grid, block, 0, s, a);
+  }
+  CB_HIP(hipGetLastError());
+  return CB_OK;
+}
+
+// Token space of a batched launch: class by class, request by request, the
+// kept tokens of request r in class c occupy [vbase, vbase + count) (arrays
+// indexed c * num_spans + r).
+struct BatchLayout {
+  std::vector<int64_t> first, count, vbase;
+  int64_t cls_base[kMaxClasses] = {0, 0, 0, 0};
+  int64_t cls_count[kMaxClasses] = {0, 0, 0, 0};
+  int64_t total = 0;
+};
+
+int batch_layout(const cb_plan* p, const cb_span* spans, int32_t num_spans, BatchLayout* L) {
+  if (num_spans < 0 || (num_spans > 0 && !spans)) return fail(CB_EINVAL, "bad request array");
+  const size_t cells = static_cast<size_t>(p->num_windows) * num_spans;
+  L->first.assign(cells, 0);
+  L->count.assign(cells, 0);
+  L->vbase.assign(cells, 0);
+  for (int r = 0; r < num_spans; ++r) {
+    const cb_span& sp = spans[r];
+    const int64_t n = sp.num_tokens;
+    if (n < 0) return fail(CB_EINVAL, "request %d: num_tokens must be >= 0", r);
+    if (sp.position_start < 0 || sp.position_start + n > p->info.table_positions)
+      return fail(CB_EINVAL, "request %d: positions [%d, %lld) exceed the RoPE table (%d positions)",
+                  r, sp.position_start, static_cast<long long>(sp.position_start + n),
+                  p->info.table_positions);
+    if (sp.source_offset < 0 || sp.target_offset < 0 || sp.source_offset > (int64_t{1} << 40) ||
+        sp.target_offset > (int64_t{1} << 40))
+      return fail(CB_EINVAL, "request %d: index offsets out of range", r);
+    if (sp.reserved != 0) return fail(CB_EINVAL, "request %d: reserved must be 0", r);
+    const int64_t prefix = sp.prefix_length > 0 ? sp.prefix_length : sp.position_start + n;
+    if (prefix < sp.position_start + n)
+      return fail(CB_EINVAL, "request %d: prefix_length is shorter than the block end", r);
+    int64_t first[kMaxClasses], count[kMaxClasses];
+    class_ranges(p, n, sp.position_start, prefix, first, count);
+    for (int c = 0; c < p->num_windows; ++c) {
+      L->first[static_cast<size_t>(c) * num_spans + r] = first[c];
+      L->count[static_cast<size_t>(c) * num_spans + r] = count[c];
+    }
+  }
+  for (int c = 0; c < p->num_windows; ++c) {
+    L->cls_base[c] = L->total;
+    for (int r = 0; r < num_spans; ++r) {
+      const size_t k = static_cast<size_t>(c) * num_spans + r;
+      L->vbase[k] = L->total;
+      L->total += L->count[k];
+    }
+    L->cls_count[c] = L->total - L->cls_base[c];
+  }
+  if (L->total > INT32_MAX) return fail(CB_EINVAL, "batch too large for one launch");
+  return CB_OK;
+}
+
+// Workspace of a batch: int32 source rows, target rows and positions of every
+// token of the batch's token space, each section 256-byte aligned.
+int64_t batch_workspace(int64_t tokens) { return 3 * ((tokens * 4 + 255) / 256 * 256); }
+
 }  // namespace
 
 extern "C" {
@@ -1543,7 +1823,6 @@ int cb_plan_get_info(const cb_plan* plan, cb_plan_info* info) {
 
 int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
   if (!p || !rq) return fail(CB_EINVAL, "null plan or request");
-  const int D = p->info.head_dim;
   const int n = rq->num_tokens;
   if (n < 1) return fail(CB_EINVAL, "num_tokens must be positive");
   if (rq->position_start < 0 ||
@@ -1553,128 +1832,104 @@ int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
                 p->info.table_positions);
   const cb_rows& sr = rq->source;
   const cb_rows& tr = rq->target;
-  if (sr.num_layers <= p->max_src_layer)
-    return fail(CB_EINVAL, "source has %d layers; the plan reads layer %d", sr.num_layers,
-                p->max_src_layer);
-  if (p->min_src_head < sr.head_offset || p->max_src_head >= sr.head_offset + sr.heads)
-    return fail(CB_EINVAL, "source rows hold heads [%d, %d); the plan reads heads %d..%d",
-                sr.head_offset, sr.head_offset + sr.heads, p->min_src_head, p->max_src_head);
-  if (tr.num_layers <= p->max_tgt_layer)
-    return fail(CB_EINVAL, "target has %d layers; the plan writes layer %d", tr.num_layers,
-                p->max_tgt_layer);
-  if (p->min_tgt_head < tr.head_offset || p->max_tgt_head >= tr.head_offset + tr.heads)
-    return fail(CB_EINVAL, "target rows hold heads [%d, %d); the plan writes heads %d..%d",
-                tr.head_offset, tr.head_offset + tr.heads, p->min_tgt_head, p->max_tgt_head);
-  if (static_cast<int64_t>(sr.heads) * D > sr.row_stride ||
-      static_cast<int64_t>(tr.heads) * D > tr.row_stride)
-    return fail(CB_EINVAL, "row_stride is smaller than heads * head_dim");
-  if (tr.index_kind == CB_INDEX_IDENTITY && sr.index_kind == CB_INDEX_IDENTITY &&
-      tr.k_base == sr.k_base && tr.k_base)
-    return fail(CB_EINVAL, "target aliases the source");
-  MapArgs a{};
   int rc;
+  if ((rc = check_sides(p, sr, tr))) return rc;
+  MapArgs a{};
   if ((rc = to_dev_rows(sr, p->elem_bytes, &a.src))) return rc;
   if ((rc = to_dev_rows(tr, p->elem_bytes, &a.tgt))) return rc;
-  const bool ws = p->info.support == 1;
-  if (ws && (sr.rows > INT32_MAX || tr.rows > INT32_MAX))
-    return fail(CB_EINVAL, "pools with more than 2^31 rows are not supported");
-  const int unit = ws ? kSubTokens : kGenSubTokens;
-  int chunk = rq->tokens_per_workgroup;
-  if (chunk == 0) chunk = default_chunk(p, n);
-  if (chunk < unit || chunk % unit)
-    return fail(CB_EINVAL, "tokens_per_workgroup must be a positive multiple of %d", unit);
-  a.w = static_cast<const uint4*>(p->d_w);
-  a.bias = p->d_bias;
-  a.jobs = p->d_jobs;
-  a.pairs = p->d_pairs;
-  a.unit_job = p->d_unit_job;
-  a.unit_njobs = p->d_unit_njobs;
-  a.unit_group = p->d_unit_group;
-  a.group_unit_start = p->d_group_unit_start;
-  a.group_unit_count = p->d_group_unit_count;
-  a.cos_tab = p->d_cos;
-  a.sin_tab = p->d_sin;
-  a.ucos_tab = p->d_ucos;
-  a.usin_tab = p->d_usin;
-  a.theta_stride = static_cast<int64_t>(p->info.table_positions) * (D / 2);
-  a.n_tokens = n;
-  a.position_start = rq->position_start;
-  a.support = p->info.support;
-  a.chunk = chunk;
-  a.err = p->d_err;
-  a.sink = p->d_sink;
   const int64_t prefix = rq->prefix_length > 0 ? rq->prefix_length
                                                : static_cast<int64_t>(rq->position_start) + n;
   if (prefix < static_cast<int64_t>(rq->position_start) + n)
     return fail(CB_EINVAL, "prefix_length is shorter than the block end");
-  int64_t items = 0;
-  a.ncls = p->num_windows;
-  for (int c = 0; c < p->num_windows; ++c) {
-    int64_t first_pos = 0;
-    if (p->window_size[c] > 0) first_pos = prefix - std::min<int64_t>(prefix, p->window_size[c] - 1);
-    const int64_t first = std::max<int64_t>(0, first_pos - rq->position_start);
-    const int64_t count = std::max<int64_t>(0, n - first);
-    const int64_t nch = (count + chunk - 1) / chunk;
-    a.cls_unit_begin[c] = p->cls_unit_begin[c];
-    a.cls_tok_first[c] = static_cast<int32_t>(std::min<int64_t>(first, n));
-    a.cls_tok_count[c] = static_cast<int32_t>(count);
-    a.cls_nchunks[c] = static_cast<int32_t>(std::max<int64_t>(nch, 1));
-    a.cls_item_begin[c] = static_cast<int32_t>(items);
-    items += static_cast<int64_t>(p->cls_unit_end[c] - p->cls_unit_begin[c]) * nch;
-  }
-  a.cls_item_begin[p->num_windows] = static_cast<int32_t>(items);
-  if (items == 0) return CB_OK;
-  if (items > (int64_t{1} << 30)) return fail(CB_EINVAL, "request too large for one launch");
-  a.total_items = static_cast<int32_t>(items);
-  a.padded_items = static_cast<int32_t>((items + 7) / 8 * 8);
-  int64_t grid_blocks = a.padded_items;
-  if (ws) {
-    // Cost line: class by class, unit weight x sub-tiles of the class.
-    int64_t cost = 0, unit_tokens = 0;
-    for (int c = 0; c < p->num_windows; ++c) {
-      const int64_t sub = (static_cast<int64_t>(a.cls_tok_count[c]) + kSubTokens - 1) / kSubTokens;
-      a.cls_unit_end[c] = p->cls_unit_end[c];
-      a.cls_subtiles[c] = static_cast<int32_t>(sub);
-      a.cls_cost_begin[c] = cost;
-      cost += (p->cls_unit_weight_end[c] - p->cls_unit_weight_begin[c]) * sub;
-      unit_tokens += static_cast<int64_t>(p->cls_unit_end[c] - p->cls_unit_begin[c]) * a.cls_tok_count[c];
-    }
-    a.cls_cost_begin[p->num_windows] = cost;
-    if (cost == 0) return CB_OK;
-    a.unit_cost_prefix = p->d_unit_cost_prefix;
-    a.num_units = p->num_units;
-    int64_t nb = p->num_cus;
-    if (rq->tokens_per_workgroup > 0)  // cap on unit-tokens per workgroup
-      nb = std::min<int64_t>(nb, std::max<int64_t>(8, (unit_tokens + chunk - 1) / chunk));
-    a.num_blocks = static_cast<int32_t>(std::max<int64_t>(8, nb / 8 * 8));
-    grid_blocks = a.num_blocks;
-    MapArgs host = a;  // cost_to_pos reads the prefix through the args
-    host.unit_cost_prefix = p->h_unit_cost_prefix.data();
-    for (int r = 0; r <= a.num_blocks; ++r) {
-      const Pos q = cost_to_pos(host, cost * r / a.num_blocks);
-      a.blk_unit[r] = q.unit;
-      a.blk_sub[r] = q.sub;
-    }
-  }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(grid_blocks)), block(ws ? kStreamThreads : kThreads);
-  if (ws) {
-    if (D == 128 && p->ntw == 2)
-      hipLaunchKernelGGL((map_install_stream_kernel<128, uint16_t>), grid, block, 0, s, a);
-    else if (D == 64 && p->ntw == 2)
-      hipLaunchKernelGGL((map_install_stream_kernel<64, uint16_t>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((map_install_stream_kernel<64, float>), grid, block, 0, s, a);
-  } else {
-    if (D == 128 && p->ntw == 2)
-      hipLaunchKernelGGL((map_install_gen_kernel<128, uint16_t>), grid, block, 0, s, a);
-    else if (D == 64 && p->ntw == 2)
-      hipLaunchKernelGGL((map_install_gen_kernel<64, uint16_t>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((map_install_gen_kernel<64, float>), grid, block, 0, s, a);
-  }
-  CB_HIP(hipGetLastError());
+  int64_t first[kMaxClasses], count[kMaxClasses];
+  class_ranges(p, n, rq->position_start, prefix, first, count);
+  a.position_start = rq->position_start;
+  return launch_map(p, a, first, count, rq->tokens_per_workgroup, default_chunk(p, n),
+                    static_cast<hipStream_t>(stream));
+}
+
+int cb_batch_workspace_bytes(const cb_plan* p, const cb_span* spans, int32_t num_spans, int64_t* bytes) {
+  if (!p || !bytes) return fail(CB_EINVAL, "null plan or output");
+  BatchLayout L;
+  int rc;
+  if ((rc = batch_layout(p, spans, num_spans, &L))) return rc;
+  *bytes = batch_workspace(L.total);
   return CB_OK;
+}
+
+int cb_map_install_batch(const cb_plan* p, const cb_rows* source, const cb_rows* target,
+                         const cb_span* spans, int32_t num_spans, void* d_workspace,
+                         int64_t workspace_bytes, void* stream) {
+  if (!p || !source || !target) return fail(CB_EINVAL, "null plan, source or target");
+  int rc;
+  if ((rc = check_sides(p, *source, *target))) return rc;
+  if (source->rows > INT32_MAX || target->rows > INT32_MAX)
+    return fail(CB_EINVAL, "batched launches address at most 2^31 rows per side");
+  BatchArgs b{};
+  if ((rc = to_dev_rows(*source, p->elem_bytes, &b.src))) return rc;
+  if ((rc = to_dev_rows(*target, p->elem_bytes, &b.tgt))) return rc;
+  BatchLayout L;
+  if ((rc = batch_layout(p, spans, num_spans, &L))) return rc;
+  for (int r = 0; r < num_spans; ++r) {
+    const int64_t n = spans[r].num_tokens;
+    const cb_rows* sides[2] = {source, target};
+    const int64_t offs[2] = {spans[r].source_offset, spans[r].target_offset};
+    for (int k = 0; k < 2; ++k)
+      if (sides[k]->index_kind == CB_INDEX_BLOCK_TABLE &&
+          sides[k]->index_offset + offs[k] + n > INT32_MAX)
+        return fail(CB_EINVAL, "request %d: block-table token offset beyond 2^31", r);
+  }
+  if (L.total == 0) return CB_OK;
+  const int64_t need = batch_workspace(L.total);
+  if (!d_workspace || workspace_bytes < need)
+    return fail(CB_EINVAL, "batch workspace of %lld bytes is smaller than the %lld needed",
+                static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  if (reinterpret_cast<uintptr_t>(d_workspace) % 256)
+    return fail(CB_EINVAL, "batch workspace must be 256-byte aligned");
+  const int64_t section = need / 3;
+  char* ws = static_cast<char*>(d_workspace);
+  b.src_row = reinterpret_cast<int32_t*>(ws);
+  b.tgt_row = reinterpret_cast<int32_t*>(ws + section);
+  b.pos = reinterpret_cast<int32_t*>(ws + 2 * section);
+  b.ncls = p->num_windows;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int r0 = 0; r0 < num_spans; r0 += kBatchSpans) {
+    b.nspans = std::min(kBatchSpans, num_spans - r0);
+    int64_t widest = 0;
+    for (int i = 0; i < b.nspans; ++i) {
+      const cb_span& sp = spans[r0 + i];
+      b.src_off[i] = sp.source_offset;
+      b.tgt_off[i] = sp.target_offset;
+      b.pos0[i] = sp.position_start;
+      for (int c = 0; c < p->num_windows; ++c) {
+        const size_t k = static_cast<size_t>(c) * num_spans + r0 + i;
+        b.first[c][i] = static_cast<int32_t>(L.first[k]);
+        b.count[c][i] = static_cast<int32_t>(L.count[k]);
+        b.vbase[c][i] = static_cast<int32_t>(L.vbase[k]);
+        widest = std::max(widest, L.count[k]);
+      }
+    }
+    if (widest == 0) continue;
+    const dim3 grid(static_cast<unsigned>((widest + 255) / 256), static_cast<unsigned>(b.nspans * b.ncls));
+    hipLaunchKernelGGL(resolve_batch_kernel, grid, dim3(256), 0, s, b);
+    CB_HIP(hipGetLastError());
+  }
+  // The map launch reads the resolved rows as int32 row vectors over the
+  // batch's token space, and each key token's position from the third section.
+  MapArgs a{};
+  a.src = b.src;
+  a.tgt = b.tgt;
+  for (DevRows* side : {&a.src, &a.tgt}) {
+    side->index_kind = CB_INDEX_I32;
+    side->index_offset = 0;
+    side->page_size = 0;
+  }
+  a.src.index = b.src_row;
+  a.tgt.index = b.tgt_row;
+  a.pos = b.pos;
+  a.position_start = 0;
+  return launch_map(p, a, L.cls_base, L.cls_count, 0,
+                    default_chunk(p, static_cast<int>(std::min<int64_t>(L.total, INT32_MAX))), s);
 }
 
 int cb_copy_rows(const cb_rows* src, const cb_rows* dst, int32_t num_layers, int32_t num_tokens,

@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .plan import HandoffPlan, Rows, ThetaSet, rows_from_page
+from .plan import HandoffPlan, RequestSpan, Rows, ThetaSet, rows_from_page
 
 
 class HeadwiseMapper:
@@ -228,6 +228,24 @@ class HeadwiseMapper:
         self.plan.launch(source, target, num_tokens=num_tokens, position_start=position_start,
                          prefix_length=prefix_length, stream=stream,
                          tokens_per_workgroup=tokens_per_workgroup)
+
+    def map_install_batch(self, source: Rows, target: Rows, spans, *,
+                          stream: torch.cuda.Stream | None = None) -> None:
+        """Fused gather -> map -> install of many requests in one launch (asynchronous).
+
+        ``spans`` are ``plan.RequestSpan`` tuples over the shared ``source`` /
+        ``target`` descriptions; every row a request writes equals what
+        ``map_install`` writes for that request alone.
+        """
+        if source.num_layers <= self._max_source_layer:
+            raise ValueError("mapper selected layer exceeds source depth")
+        self._check_source_heads(source.c.head_offset, source.c.heads)
+        for sp in spans:
+            sp = RequestSpan(*sp)
+            if sp.num_tokens < 0:
+                raise ValueError("a request cannot have a negative token count")
+            self._check_positions(sp.position_start, sp.num_tokens)
+        self.plan.launch_batch(source, target, spans, stream=stream)
 
 
 class PageMapper(HeadwiseMapper):

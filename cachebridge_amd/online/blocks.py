@@ -12,6 +12,8 @@ Same names, argument meaning and error behaviour as the reference primitives
   intermediate mapped tensor.
 - ``map_install_block``: gather + map + install straight from the source pool
   (no packed block at all), through a token-slot vector or a block table.
+- ``map_install_batch``: the same for a ragged batch of requests (an admitted
+  cohort, ``cb/online/admission.py:420-499``) in one launch.
 - ``install_unpublished``: allocate, write all blocks in order, vote, then
   publish or roll back (``cb/online/blocks.py:114-171``).
 """
@@ -20,7 +22,7 @@ from __future__ import annotations
 
 import torch
 
-from ..plan import rows_from_page, copy_rows
+from ..plan import RequestSpan, copy_rows, rows_from_page
 from ..pool import pool_rows
 
 
@@ -141,6 +143,43 @@ def map_install_block(mapper, source_pool, source_indices, target_pool, *, start
     mapper.map_install(source, target, num_tokens=n, position_start=start,
                        prefix_length=prefix_length, stream=stream,
                        tokens_per_workgroup=tokens_per_workgroup)
+
+
+def map_install_batch(mapper, source_pool, source_indices, target_pool, requests, *,
+                      target_indices=None, block_table=None, page_size=None,
+                      source_head_offset=0, stream=None):
+    """Gather, map and install every request of a ragged batch in one launch.
+
+    ``requests`` are ``RequestSpan(source_offset, target_offset, num_tokens,
+    position_start, prefix_length)``: request token ``t`` reads source row
+    ``source_indices[source_offset + t]`` and writes target row
+    ``target_indices[target_offset + t]``, or, with ``block_table``, target
+    row ``bt[u // ps] * ps + u % ps`` at ``u = target_offset + t`` (so a
+    request whose pages start at block-table entry ``e`` has
+    ``target_offset = e * ps``). Every row equals what ``map_install_block``
+    writes for that request alone. Asynchronous on ``stream``.
+    """
+    spans = [RequestSpan(*r) for r in requests]
+    if (target_indices is None) == (block_table is None):
+        raise ValueError("give exactly one of target_indices or block_table")
+    if target_pool.layer_num != mapper.target_layers:
+        raise ValueError("mapper output geometry/dtype mismatch")
+    for sp in spans:
+        if sp.num_tokens < 0 or sp.source_offset < 0 or sp.target_offset < 0:
+            raise ValueError("invalid request span")
+    src_end = max((sp.source_offset + sp.num_tokens for sp in spans if sp.num_tokens), default=0)
+    tgt_end = max((sp.target_offset + sp.num_tokens for sp in spans if sp.num_tokens), default=0)
+    if src_end > len(source_indices):
+        raise ValueError("a request reads past the end of source_indices")
+    source = pool_rows(source_pool, index=source_indices, head_offset=source_head_offset)
+    if block_table is not None:
+        ps = page_size if page_size is not None else getattr(target_pool, "page_size", None)
+        target = pool_rows(target_pool, block_table=block_table, page_size=ps, tokens=tgt_end)
+    else:
+        if tgt_end > len(target_indices):
+            raise ValueError("a request writes past the end of target_indices")
+        target = pool_rows(target_pool, index=target_indices)
+    mapper.map_install_batch(source, target, spans, stream=stream)
 
 
 def install_unpublished(*, token_count, allocate, free, blocks, write, synchronize, ready_vote,

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
-from typing import Sequence
+from typing import NamedTuple, Sequence
 
 import numpy as np
 import torch
@@ -177,6 +177,36 @@ def _ptr(a: np.ndarray):
     return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
 
 
+class RequestSpan(NamedTuple):
+    """One request of a batched launch (``cb_span``).
+
+    Token ``t`` (``0 <= t < num_tokens``) sits at position
+    ``position_start + t``; its source row is the shared source description's
+    row of ``u = source_offset + t`` and its target row likewise with
+    ``target_offset``. ``prefix_length`` (0: ``position_start + num_tokens``)
+    is the whole prefix for sliding-window classes.
+    """
+
+    source_offset: int
+    target_offset: int
+    num_tokens: int
+    position_start: int = 0
+    prefix_length: int = 0
+
+
+def _span_array(spans: Sequence[RequestSpan]):
+    arr = (_lib.CbSpan * max(1, len(spans)))()
+    for i, sp in enumerate(spans):
+        sp = RequestSpan(*sp)
+        arr[i].source_offset = int(sp.source_offset)
+        arr[i].target_offset = int(sp.target_offset)
+        arr[i].num_tokens = int(sp.num_tokens)
+        arr[i].position_start = int(sp.position_start)
+        arr[i].prefix_length = int(sp.prefix_length)
+        arr[i].reserved = 0
+    return arr
+
+
 class HandoffPlan:
     """Owner of one device-resident ``cb_plan`` (see ``include/cachebridge_hip.h``).
 
@@ -301,6 +331,43 @@ class HandoffPlan:
         req.tokens_per_workgroup = int(tokens_per_workgroup)
         _lib.check(self.lib.cb_map_install(self._handle, ctypes.byref(req),
                                            _lib.stream_handle(stream)))
+
+    def workspace_bytes(self, spans: Sequence[RequestSpan]) -> int:
+        """Device workspace bytes of a batched launch over ``spans``."""
+        if self._handle is None:
+            raise RuntimeError("plan is closed")
+        total = ctypes.c_int64(0)
+        arr = _span_array(spans)
+        _lib.check(self.lib.cb_batch_workspace_bytes(self._handle, arr, len(spans), ctypes.byref(total)))
+        return int(total.value)
+
+    def launch_batch(self, source: Rows, target: Rows, spans: Sequence[RequestSpan], *,
+                     stream: torch.cuda.Stream | None = None) -> None:
+        """Enqueue the map + install of every request in ``spans`` as one launch (asynchronous).
+
+        The int32 workspace (source row, target row and position of every kept
+        token) comes from torch's caching allocator and is recorded on the
+        launch stream, so it is not reused before the launch completes.
+        """
+        if self._handle is None:
+            raise RuntimeError("plan is closed")
+        if source.dtype != self.dtype or target.dtype != self.dtype:
+            raise ValueError(f"source/target dtype must be {self.dtype}")
+        if source.device != self.device or target.device != self.device:
+            raise ValueError("source, target and plan must be on the same device")
+        arr = _span_array(spans)
+        total = ctypes.c_int64(0)
+        _lib.check(self.lib.cb_batch_workspace_bytes(self._handle, arr, len(spans), ctypes.byref(total)))
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        workspace = None
+        ptr = None
+        if total.value > 0:
+            with torch.cuda.stream(s):
+                workspace = torch.empty(int(total.value), dtype=torch.uint8, device=self.device)
+            ptr = workspace.data_ptr()
+        _lib.check(self.lib.cb_map_install_batch(self._handle, ctypes.byref(source.c),
+                                                 ctypes.byref(target.c), arr, len(spans), ptr,
+                                                 int(total.value), _lib.stream_handle(s)))
 
     def read_errors(self, stream: torch.cuda.Stream | None = None) -> int:
         """Synchronize ``stream`` and return/clear the device out-of-range flags."""

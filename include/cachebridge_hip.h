@@ -171,6 +171,43 @@ int cb_plan_get_info(const cb_plan* plan, cb_plan_info* info);
    scatter for every job of the plan over one request block. Asynchronous. */
 int cb_map_install(const cb_plan* plan, const cb_request* request, void* stream);
 
+/*
+ * One request of a batched launch: tokens [0, num_tokens) of its history at
+ * positions position_start + t. Its source row of token t is the shared
+ * source description's row of u = source_offset + t (the cb_rows index
+ * rules, including that description's index_offset), and likewise for the
+ * target. With SGLang's req_to_token table, for example, the offsets are the
+ * request's row times the table's row length.
+ */
+typedef struct cb_span {
+  int64_t source_offset;
+  int64_t target_offset;
+  int32_t num_tokens;     /* >= 0; a request with 0 tokens is skipped */
+  int32_t position_start; /* >= 0 */
+  int32_t prefix_length;  /* whole prefix for windows; 0 means position_start + num_tokens */
+  int32_t reserved;       /* 0 */
+} cb_span;
+
+/* Device workspace bytes cb_map_install_batch needs for these spans (host
+   array). */
+int cb_batch_workspace_bytes(const cb_plan* plan, const cb_span* spans, int32_t num_spans,
+                             int64_t* bytes);
+
+/* Every job of the plan over every request of a ragged batch, as one map
+   launch (after one small launch per 32 requests that resolves each kept
+   token's source row, target row and position into the workspace). Same
+   results, row for row, as one cb_map_install per request. `spans` is a host
+   array (read before the call returns); `d_workspace` is caller-owned device
+   memory of at least cb_batch_workspace_bytes bytes, 256-byte aligned, that
+   no other launch may use until this one completes. Asynchronous.
+   Replaces the reference's one-request-at-a-time mapper transactions over an
+   admitted cohort (begin_next_mapper / publish_active_mapper,
+   cb/online/admission.py:466-499), each a map_page + install
+   (cb/online/blocks.py:86-111). */
+int cb_map_install_batch(const cb_plan* plan, const cb_rows* source, const cb_rows* target,
+                         const cb_span* spans, int32_t num_spans, void* d_workspace,
+                         int64_t workspace_bytes, void* stream);
+
 /* Copy the first row_elements elements of rows of layers [0, num_layers)
    from src to dst, K and V: dst layer l row dst_row(t) <- src layer l row
    src_row(t) for t in [0, num_tokens). row_elements * element size must be a

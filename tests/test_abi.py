@@ -88,7 +88,7 @@ def _compile_and_run(gcc, struct, fields):
 
 
 @pytest.mark.parametrize("cls,cname", [(_lib.CbRows, "cb_rows"), (_lib.CbPlanDesc, "cb_plan_desc"),
-                                       (_lib.CbRequest, "cb_request"),
+                                       (_lib.CbRequest, "cb_request"), (_lib.CbSpan, "cb_span"),
                                        (_lib.CbPlanInfo, "cb_plan_info")])
 def test_struct_layouts_match_the_c_compiler(cls, cname):
     fields = [name for name, _ in cls._fields_]
@@ -108,6 +108,10 @@ def test_host_validation_errors_without_a_device(lib):
     assert rc == _lib.CB_EINVAL and b"16" in lib.cb_last_error()
     with pytest.raises(ValueError, match="null"):
         _lib.check(lib.cb_map_install(None, None, None))
+    with pytest.raises(ValueError, match="null"):
+        _lib.check(lib.cb_map_install_batch(None, None, None, None, 0, None, 0, None))
+    total = ctypes.c_int64(0)
+    assert lib.cb_batch_workspace_bytes(None, None, 0, ctypes.byref(total)) == _lib.CB_EINVAL
     assert lib.cb_plan_create(None, None) == _lib.CB_EINVAL
     info = _lib.CbPlanInfo()
     assert lib.cb_plan_get_info(None, ctypes.byref(info)) == _lib.CB_EINVAL
