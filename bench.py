@@ -42,6 +42,11 @@ WORKLOADS = {
             "128, 4096 tokens, bf16, page 16, 8192-page target pool",
     "full32k": "Qwen3-14B->32B whole model, long history: source 40x8 -> target 64x8 KV heads, "
                "head_dim 128, 32768 tokens, bf16, page 16, 4096-page target pool",
+    "batch": "64 ragged requests (lognormal lengths, median 2048, sigma 0.5, clipped to [256, 16384]; "
+             "137,440 tokens) in one launch at the Qwen3-14B->32B TP4 share (40x2 -> 64x2 KV heads, "
+             "head_dim 128, bf16) into a shared 0.92 M-slot target pool at 85% occupancy (page 16)",
+    "batch_full": "the same 64 ragged requests in one launch at the whole-model geometry (40x8 -> 64x8 "
+                  "KV heads, head_dim 128, bf16) into a shared target pool at 50% occupancy (page 16)",
     "gemma": "Gemma-3-style target: source 40x8 -> target 62x16 KV heads (10 global layers keep all "
              "8192 tokens, 52 sliding-window layers keep the last 1023), head map h_src = h // 2, "
              "theta 1e4 local / 1e6 global, head_dim 128, bf16, page 16",
@@ -192,7 +197,10 @@ def main() -> int:
 
     torch.cuda.set_device(0)
     sh = synthetic.shape(args.workload, tokens=args.tokens)
-    h = synthetic.make_handoff(sh)
+    if args.workload.startswith("batch"):
+        h = synthetic.make_batch_handoff(sh)
+    else:
+        h = synthetic.make_handoff(sh)
     wall, kernel_ms, kernel_min = time_handoff(h, args.steps, args.warmup, args.tokens_per_workgroup)
     tokens = sh.tokens
     value = args.steps * tokens / wall
@@ -220,7 +228,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic("map_install_stream", args.workload),
-                     "kernel": "map_install_stream_kernel<128, bf16>",
+                     "kernel": ("resolve_batch_kernel + map_install_stream_kernel<128, bf16, "
+                                "per-token positions>" if args.workload.startswith("batch")
+                                else "map_install_stream_kernel<128, bf16>"),
                      "algorithmic_bytes_per_launch": bytes_alg,
                      "kernel_ms_mean": round(kernel_ms, 5), "kernel_ms_min": round(kernel_min, 5)},
         "mfma": {"algorithmic_tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 2),

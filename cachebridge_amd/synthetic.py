@@ -14,7 +14,12 @@ Shapes (source model -> target model, per GPU):
                sliding window 1024 on local layers, head map h_src = h // 2,
                8192 tokens, theta 1e4 local / 1e6 global.
 - ``batch``:   64 ragged requests (lognormal lengths, median 2048, sigma 0.5,
-               clipped to [256, 16384]) into one shared pool at 85% occupancy.
+               clipped to [256, 16384]; 137,440 tokens) at the TP4 share
+               (40x2 -> 64x2) into one shared target pool at 85% occupancy
+               (0.99 M slots; the 64x8 pool at that occupancy would need
+               260 GB next to the source pool, more than one GPU holds).
+- ``batch_full``: the same requests at the whole-model 64x8 geometry, with the
+               target pool at 50% occupancy (2x the batch's pages).
 
 Source keys are treated as stored RoPE-rotated (as SGLang stores them); the
 map is A ~ N(0, 1/(s*D)), b ~ N(0, 0.01); bf16 sources are N(0,1) times a
@@ -69,11 +74,23 @@ def shape(name: str, tokens: int | None = None) -> Shape:
                   target_theta=[1e6 if g else 1e4 for g in glob],
                   windows=[None if g else 1024 for g in glob], head_map="half",
                   target_pages=1024, seed=5)
+    elif name in ("batch", "batch_full"):
+        heads = 2 if name == "batch" else 8
+        s = Shape(name, 40, heads, 64, heads, 128, sum(request_lengths()), torch.bfloat16, sel16,
+                  seed=6 if name == "batch" else 7)
     else:
         raise ValueError(f"unknown workload shape {name!r}")
     if tokens is not None:
         s.tokens = tokens
     return s
+
+
+def request_lengths(count: int = 64, median: int = 2048, sigma: float = 0.5, lo: int = 256,
+                    hi: int = 16384, seed: int = 77) -> list[int]:
+    """Seeded ragged request lengths: round(median * exp(sigma * N(0,1))) clipped to [lo, hi]."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.exp(torch.randn(count, generator=g, dtype=torch.float64) * sigma) * median
+    return x.round().clamp(lo, hi).long().tolist()
 
 
 def _gen(seed: int) -> torch.Generator:
@@ -220,3 +237,76 @@ def algorithmic_flops(sh: Shape) -> int:
     d = sh.head_dim
     return sum(2 * 2 * window_tokens(sh, l) * sh.target_heads * d * d
                for l in range(sh.target_layers))
+
+
+@dataclass
+class BatchHandoff:
+    """A resident ragged batch: one source pool, one shared target pool, one span per request."""
+
+    shape: Shape
+    spec: dict
+    mapper: HeadwiseMapper
+    source_pool: PagedKVPool
+    source_slots: torch.Tensor     # int32, the requests' source slots back to back
+    target_pool: PagedKVPool
+    block_table: torch.Tensor      # int32, the requests' pages back to back
+    spans: list                    # plan.RequestSpan per request
+    lengths: list
+
+    @property
+    def tokens(self) -> int:
+        return sum(self.lengths)
+
+    def run(self, *, stream=None, tokens_per_workgroup=0):
+        from .online.blocks import map_install_batch
+
+        if tokens_per_workgroup:
+            raise ValueError("batched launches use one workgroup per CU")
+        map_install_batch(self.mapper, self.source_pool, self.source_slots, self.target_pool,
+                          self.spans, block_table=self.block_table,
+                          page_size=self.shape.page_size, stream=stream)
+
+
+def make_batch_handoff(sh: Shape, lengths: list | None = None, *, occupancy: float | None = None,
+                       device="cuda") -> BatchHandoff:
+    """Requests of ``lengths`` tokens (whole histories at positions 0..n-1) in shared pools.
+
+    The target pool is sized so that the batch's pages are the free
+    ``1 - occupancy`` of it, drawn from a seeded shuffled free list. Source
+    values are drawn on the device from a seeded generator (bf16 N(0,1) times
+    the per-channel lognormal scale), which keeps multi-GB pools fast to build.
+    """
+    from .plan import RequestSpan
+
+    lengths = list(lengths if lengths is not None else request_lengths())
+    if occupancy is None:
+        occupancy = 0.85 if sh.name == "batch" else 0.5
+    ps = sh.page_size
+    total = sum(lengths)
+    spec = mapper_spec(sh)
+    mapper = make_mapper(sh, spec, device=device, max_positions=max(40960, max(lengths)))
+    need = sum((n + ps - 1) // ps for n in lengths)
+    src_total = need * 2
+    src_pool = PagedKVPool(layer_num=sh.source_layers, pages=src_total, head_num=sh.source_heads,
+                           head_dim=sh.head_dim, page_size=ps, dtype=sh.dtype, device=device)
+    g = torch.Generator(device=device).manual_seed(5000 + sh.seed)
+    scale = torch.exp(torch.randn(sh.head_dim, generator=_gen(2000 + sh.seed)) * 0.5).to(device)
+    src_pages = fragmented_pages(src_total, need, 3000 + sh.seed)
+    slots, spans, entry, off = [], [], 0, 0
+    for n in lengths:
+        k = (n + ps - 1) // ps
+        slots.append(slots_from_pages(src_pages[entry:entry + k], n, ps))
+        spans.append(RequestSpan(off, entry * ps, n, 0, 0))
+        entry += k
+        off += n
+    src_slots = torch.cat(slots).to(device)
+    for l in range(sh.source_layers):
+        for buf in (src_pool.k_buffer[l], src_pool.v_buffer[l]):
+            x = torch.randn((total, sh.source_heads, sh.head_dim), generator=g, device=device)
+            buf[src_slots] = (x * scale).to(sh.dtype)
+    pages = max(int(math.ceil(need / (1.0 - occupancy))), need)
+    tgt_pool = PagedKVPool(layer_num=sh.target_layers, pages=pages, head_num=sh.target_heads,
+                           head_dim=sh.head_dim, page_size=ps, dtype=sh.dtype, device=device)
+    bt = fragmented_pages(pages, need, 4000 + sh.seed).to(device)
+    return BatchHandoff(sh, spec, mapper, src_pool, src_slots.to(torch.int32), tgt_pool, bt,
+                        spans, lengths)

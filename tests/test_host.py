@@ -88,3 +88,30 @@ def test_bench_refuses_more_than_one_gpu():
                          capture_output=True, text=True, timeout=120)
     assert out.returncode == 2
     assert "one GPU" in out.stderr
+
+
+def test_ragged_batch_lengths_and_bytes():
+    lengths = synthetic.request_lengths()
+    assert len(lengths) == 64 and sum(lengths) == 137_440
+    assert all(256 <= n <= 16384 for n in lengths)
+    assert synthetic.request_lengths() == lengths  # seeded
+    clipped = synthetic.request_lengths(count=2000, sigma=2.0)
+    assert min(clipped) == 256 and max(clipped) == 16384
+    for name, heads in (("batch", 2), ("batch_full", 8)):
+        sh = synthetic.shape(name)
+        assert (sh.target_heads, sh.tokens) == (heads, 137_440)
+        pairs = _distinct_pairs(sh)
+        t, d = sh.tokens, sh.head_dim
+        closed = (2 * 2 * d * 64 * heads * t + 2 * 2 * d * pairs * t
+                  + 4 * 2 * 64 * heads * (d * d + d) + 8 * t)
+        assert synthetic.algorithmic_bytes(sh) == closed
+
+
+def test_request_span_defaults():
+    from cachebridge_amd.plan import RequestSpan, _span_array
+
+    sp = RequestSpan(10, 32, 5)
+    assert (sp.position_start, sp.prefix_length) == (0, 0)
+    arr = _span_array([sp, (0, 0, 0, 7, 9)])
+    assert (arr[0].source_offset, arr[0].target_offset, arr[0].num_tokens) == (10, 32, 5)
+    assert (arr[1].position_start, arr[1].prefix_length, arr[1].reserved) == (7, 9, 0)
