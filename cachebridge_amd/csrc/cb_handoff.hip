@@ -63,8 +63,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // outstanding HBM traffic, so every pool/table access goes through these.
 #if defined(__HIP_DEVICE_COMPILE__)
 #define CB_GLOBAL __attribute__((address_space(1)))
+#define CB_CONST __attribute__((address_space(4)))
+#define CB_LDS __attribute__((address_space(3)))
 #else
 #define CB_GLOBAL
+#define CB_CONST
+#define CB_LDS
 #endif
 typedef const CB_GLOBAL char* gcptr;
 typedef CB_GLOBAL char* gptr;
@@ -75,6 +79,14 @@ __device__ inline V gload(gcptr p) {
 template <typename V>
 __device__ inline void gstore(gptr p, const V& v) {
   *reinterpret_cast<CB_GLOBAL V*>(p) = v;
+}
+// Plan metadata (job, unit and pair tables, layer pointer arrays) is read-only
+// for a launch: loading it through the constant address space lets the
+// compiler use scalar loads for wave-uniform indices instead of vector loads
+// whose results would have to wait for every older vector load.
+template <typename V>
+__device__ inline V cload(const V* p) {
+  return *(const CB_CONST V*)(p);
 }
 __device__ inline gcptr as_global(const void* p) { return (gcptr)p; }
 __device__ inline gptr as_global(void* p) { return (gptr)p; }
@@ -285,7 +297,7 @@ __device__ inline int64_t row_finish(const DevRows& R, int t, uint2 f) {
 
 __device__ inline gcptr layer_base(const DevRows& R, int kind, int layer) {
   const void* const* arr = kind ? R.v_layers : R.k_layers;
-  if (arr) return as_global(*reinterpret_cast<const CB_GLOBAL void* const CB_GLOBAL*>(as_global(arr + layer)));
+  if (arr) return as_global(cload(arr + layer));
   return as_global(kind ? R.v_base : R.k_base) + layer * R.layer_stride_b;
 }
 
@@ -366,8 +378,8 @@ __device__ inline bool decode_work(const MapArgs& a, Work* w) {
   const int r = lc - (us - ub) * nch;
   const int chunk_id = r / un;
   const int unit = us + r % un;
-  w->job = a.unit_job[unit];
-  w->njobs = a.unit_njobs[unit];
+  w->job = cload(a.unit_job + unit);
+  w->njobs = cload(a.unit_njobs + unit);
   w->tok_lo = a.cls_tok_first[c] + chunk_id * a.chunk;
   w->tok_hi = min(w->tok_lo + a.chunk, a.cls_tok_first[c] + a.cls_tok_count[c]);
   return true;
@@ -523,19 +535,22 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   const int g = lane >> 4;
   const int col = lane & 15;
 
-  const int4 meta0 = a.jobs[wk.job];
-  const int sth = (meta0.y >> 16) & 0xff;
-  const int tth = (meta0.y >> 24) & 0xff;
-  const int pr = a.pairs[wk.job];
+  // Job metadata: scalar loads at a wave-uniform index.
+  const int job = __builtin_amdgcn_readfirstlane(wk.job);
+  const int* jm = reinterpret_cast<const int*>(a.jobs + job);  // int4 per job: x, y, z, w
+  const int meta_y = cload(jm + 1);
+  const int sth = (meta_y >> 16) & 0xff;
+  const int tth = (meta_y >> 24) & 0xff;
+  const int pr = cload(a.pairs + job);
   const int sl = pr & 0xffff;
   const int sh = pr >> 16;
 
   gptr tbase[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int4 m = a.jobs[wk.job + j];
-    tbase[j] = const_cast<gptr>(layer_base(a.tgt, kind, m.x & 0xffff)) +
-               static_cast<int64_t>((m.x >> 16) - a.tgt.head_offset) * D * C::BYTES;
+    const int mx = cload(jm + 4 * j);
+    tbase[j] = const_cast<gptr>(layer_base(a.tgt, kind, mx & 0xffff)) +
+               static_cast<int64_t>((mx >> 16) - a.tgt.head_offset) * D * C::BYTES;
   }
   // Stores of tokens without a target row go to a scratch sink, so every
   // iteration issues a fixed number of memory operations (the compiler can
@@ -583,15 +598,16 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     }
   };
 
-  // Source dims and un-rotation tables of the next two sub-tiles (stage = k & 1
-  // for this wave's k-th sub-tile).
-  uint4 xr[2][CT][2][C::RUN_U4];
-  float uc[2][CT][TG], us[2][CT][TG];
-  bool live_x[2][CT];
-  auto prefetch = [&](int st, int sub, const int32_t (&srow)[CT], const int32_t (&prow)[CT]) {
+  // Source dims and un-rotation tables of the next sub-tile of this wave,
+  // requested one sub-tile ahead (a sub-tile is about a microsecond of one
+  // wave's time, which covers the load latency).
+  uint4 xr[CT][2][C::RUN_U4];
+  float uc[CT][TG], us[CT][TG];
+  bool live_x[CT];
+  auto prefetch = [&](int sub, const int32_t (&srow)[CT], const int32_t (&prow)[CT]) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      live_x[st][ct] = srow[ct] >= 0;
+      live_x[ct] = srow[ct] >= 0;
       // Rows without a source read row 0 (always valid) and are zeroed on use.
       const int64_t r = srow[ct] >= 0 ? srow[ct] : 0;
       gcptr p = sbase + r * a.src.row_stride_b + g * G * C::BYTES;
@@ -599,86 +615,69 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int u = 0; u < C::RUN_U4; ++u)
-          xr[st][ct][h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
+          xr[ct][h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
       if constexpr (IS_K) {
         const int64_t off = static_cast<int64_t>(PV ? prow[ct] : a.position_start + token_of(sub, ct)) * HALF;
-        load_tab<G>(ucos + off, g, uc[st][ct]);
-        load_tab<G>(usin + off, g, us[st][ct]);
+        load_tab<G>(ucos + off, g, uc[ct]);
+        load_tab<G>(usin + off, g, us[ct]);
       }
     }
   };
-  auto dummy_stores = [&]() {
-    float zero[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) zero[e] = 0.f;
-#pragma unroll
-    for (int i = 0; i < NJ * NGRP * CT; ++i) {
-      store_elems<IO, 8>(sink, zero);
-      store_elems<IO, 8>(sink + HALF * C::BYTES, zero);
-    }
-  };
 
-  // Sub-tiles are claimed in order by each wave: its first four statically
-  // (wave + 8k), the rest from a workgroup counter in LDS as the wave moves
-  // along, so faster waves take more of the segment and all waves finish
-  // within about one sub-tile of each other. Claims past the segment end are
-  // dead (masked, no MFMAs). A claim is made when its index loads are issued,
-  // four sub-tiles ahead of its multiply.
+  // Sub-tiles are claimed in order by each wave: its first two statically
+  // (wave, wave + 8), the rest from a workgroup counter in LDS as the wave
+  // moves along, so faster waves take more of the segment and all waves
+  // finish within about one sub-tile of each other. A claim is made when its
+  // index loads are issued, two sub-tiles ahead of its multiply.
   constexpr int SW = kStreamWaves;
-  constexpr int kStatic = 4 * SW;
-  int c0 = wave, c1 = wave + SW, c2 = wave + 2 * SW, c3 = wave + 3 * SW;  // claim pipeline
+  constexpr int kStatic = 2 * SW;
+  int c0 = wave, c1 = wave + SW;  // current and next sub-tile
   auto claim = [&]() {  // one claim per wave, broadcast to all lanes
     int v = 0;
     if (lane == 0) v = atomicAdd(lds_next, 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
 
-  // Segment start: the unit's W and bias, the first rows and the first two
-  // sub-tiles are requested before waiting for the workgroup's previous
-  // segment to release LDS, so their latency overlaps that segment's tail.
-  int32_t sr0[CT], sr1[CT], tr_a[CT], tr_b[CT], pr0[CT], pr1[CT];
-  int32_t pr_a[CT], pr_b[CT];                    // positions of the current and next sub-tile (batched keys)
-  uint2 fs_a[CT], fd_a[CT], fs_b[CT], fd_b[CT];  // index loads of sub-tiles +2 and +3 ahead
-  int32_t fp_a[CT], fp_b[CT];                    // their position words (batched keys)
-  fetch_rows(c0, fs_a, fd_a, fp_a);
-  fetch_rows(c1, fs_b, fd_b, fp_b);
+  // Segment start: the first two sub-tiles' rows and the first one's source
+  // dims are requested before waiting for the workgroup's previous segment
+  // to release LDS, so their latency overlaps that segment's tail.
+  int32_t sr0[CT], tr_a[CT], pr_a[CT];           // rows / positions of the current sub-tile
+  uint2 fs_b[CT], fd_b[CT];                      // index words of the next sub-tile
+  int32_t fp_b[CT];                              // its position words (batched keys)
+  {
+    uint2 fs_a[CT], fd_a[CT];
+    int32_t fp_a[CT];
+    fetch_rows(c0, fs_a, fd_a, fp_a);
+    fetch_rows(c1, fs_b, fd_b, fp_b);
+    finish_rows(c0, fs_a, fd_a, fp_a, sr0, tr_a, pr_a);
+  }
   constexpr int WPER = NJ * C::W_U4 / kStreamThreads;
   static_assert(NJ * C::W_U4 % kStreamThreads == 0 && NJ * D <= kStreamThreads, "staging split");
-  uint4 wreg[WPER];
-  {
-    gcptr wsrc = as_global(a.w + static_cast<size_t>(wk.job) * C::W_U4);
-#pragma unroll
-    for (int i = 0; i < WPER; ++i) wreg[i] = gload<uint4>(wsrc + (i * kStreamThreads + threadIdx.x) * 16);
-  }
-  const float breg = threadIdx.x < NJ * D ? a.bias[static_cast<size_t>(wk.job) * D + threadIdx.x] : 0.f;
-  finish_rows(c0, fs_a, fd_a, fp_a, sr0, tr_a, pr0);
-  finish_rows(c1, fs_b, fd_b, fp_b, sr1, tr_b, pr1);
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) {
-    pr_a[ct] = pr0[ct];
-    pr_b[ct] = pr1[ct];
-  }
-  // Outstanding at loop entry, oldest first, as after any iteration:
-  // x(k), rows(k+2), stores, x(k+1), rows(k+3), stores.
-  prefetch(0, c0, sr0, pr0);
-  fetch_rows(c2, fs_a, fd_a, fp_a);
+  const float breg = threadIdx.x < NJ * D ? a.bias[static_cast<size_t>(job) * D + threadIdx.x] : 0.f;
+  prefetch(c0, sr0, pr_a);
   __syncthreads();  // the previous segment no longer reads LDS (nor claims)
+  // The unit's W goes straight from memory into LDS (16 bytes per lane, each
+  // wave filling 1 KB runs), with no register staging. Waiting for every
+  // older load here costs little: W is the last thing requested, and the
+  // loop then starts with nothing outstanding.
+  {
+    gcptr wsrc = as_global(a.w + static_cast<size_t>(job) * C::W_U4);
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
-  for (int i = 0; i < WPER; ++i) lds_w[i * kStreamThreads + threadIdx.x] = wreg[i];
+    for (int i = 0; i < WPER; ++i)
+      __builtin_amdgcn_global_load_lds(wsrc + (i * kStreamThreads + threadIdx.x) * 16,
+                                       (CB_LDS void*)(lds_w + i * kStreamThreads + wv * kWave), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+  }
   if (threadIdx.x < NJ * D) lds_bias[threadIdx.x] = breg;
   if (threadIdx.x == 0) *lds_next = kStatic;
-  dummy_stores();
-  prefetch(1, c1, sr1, pr1);
-  fetch_rows(c3, fs_b, fd_b, fp_b);
   __syncthreads();  // W, bias and claim counter ready
-  dummy_stores();
 
-  // One sub-tile of this wave; the prefetch stage is a compile-time constant
-  // (register arrays indexed at run time would be placed in scratch memory).
-  // Sub-tiles past the segment run masked (rows -1) and skip their MFMAs.
-  auto body = [&](auto stage, int sub) {
-    constexpr int st = decltype(stage)::value;
-    const bool alive = sub < nsub;
+  // One sub-tile of this wave. Outstanding at its start, oldest first: its
+  // source dims, the next sub-tile's index words, the previous one's stores,
+  // so each wait covers only what it needs.
+  while (c0 < nsub) {
+    const int sub = c0;
     // W fragments are re-read from LDS every sub-tile: keep the compiler from
     // hoisting them into registers.
     asm volatile("" ::: "memory");
@@ -697,26 +696,26 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       float x1[G], x2[G];
 #pragma unroll
       for (int u = 0; u < C::RUN_U4; ++u) {
-        unpack16<IO>(xr[st][ct][0][u], x1 + u * C::E16);
-        unpack16<IO>(xr[st][ct][1][u], x2 + u * C::E16);
+        unpack16<IO>(xr[ct][0][u], x1 + u * C::E16);
+        unpack16<IO>(xr[ct][1][u], x2 + u * C::E16);
       }
       if constexpr (IS_K) {
 #pragma unroll
         for (int e = 0; e < G; ++e) {
-          const float k1 = x1[e] * uc[st][ct][e] + x2[e] * us[st][ct][e];
-          const float k2 = x2[e] * uc[st][ct][e] - x1[e] * us[st][ct][e];
+          const float k1 = x1[e] * uc[ct][e] + x2[e] * us[ct][e];
+          const float k2 = x2[e] * uc[ct][e] - x1[e] * us[ct][e];
           x1[e] = k1;
           x2[e] = k2;
         }
         if constexpr (SHARED) {
 #pragma unroll
           for (int e = 0; e < G; ++e) {
-            tc[ct][e] = uc[st][ct][e];
-            ts[ct][e] = us[st][ct][e];
+            tc[ct][e] = uc[ct][e];
+            ts[ct][e] = us[ct][e];
           }
         }
       }
-      if (!live_x[st][ct]) {
+      if (!live_x[ct]) {
 #pragma unroll
         for (int e = 0; e < G; ++e) x1[e] = x2[e] = 0.f;
       }
@@ -730,31 +729,20 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
           bx[ct][ks][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
       }
     }
-    // The sub-tile two ahead: resolve its rows, request its source dims into
-    // the stage just consumed, and claim the sub-tile four ahead and issue
-    // its index loads.
+    // The next sub-tile: resolve its rows and request its source dims into
+    // the registers just consumed; claim the one after it and issue its
+    // index loads.
+    int c2;
     {
-      int32_t sr2[CT], tr2[CT], pr2[CT];
-      finish_rows(c2, fs_a, fd_a, fp_a, sr2, tr2, pr2);
-      prefetch(st, c2, sr2, pr2);
+      int32_t sr1[CT], tr1[CT], pr1[CT];
+      finish_rows(c1, fs_b, fd_b, fp_b, sr1, tr1, pr1);
+      prefetch(c1, sr1, pr1);
+      c2 = claim();
+      fetch_rows(c2, fs_b, fd_b, fp_b);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        fs_a[ct] = fs_b[ct];
-        fd_a[ct] = fd_b[ct];
-        fp_a[ct] = fp_b[ct];
-      }
-      const int c4 = claim();
-      fetch_rows(c4, fs_b, fd_b, fp_b);
-      c0 = c1;
-      c1 = c2;
-      c2 = c3;
-      c3 = c4;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        tr_a[ct] = tr_b[ct];
-        tr_b[ct] = tr2[ct];
-        pr_a[ct] = pr_b[ct];
-        pr_b[ct] = pr2[ct];
+        tr_a[ct] = tr1[ct];
+        pr_a[ct] = pr1[ct];
       }
     }
 
@@ -781,7 +769,7 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
           for (int w = 0; w < NTW; ++w)
             dst[w] = __builtin_bit_cast(bf16x8, wj[((rt * KS + ks) * NTW + w) * kWave + lane]);
         };
-        if (alive) {
+        {
           read_w(0, ring[0]);
           read_w(1, ring[1]);
 #pragma unroll
@@ -838,10 +826,8 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
         }
       }
     }
-  };
-  while (c0 < nsub) {
-    body(std::integral_constant<int, 0>{}, c0);
-    body(std::integral_constant<int, 1>{}, c0);
+    c0 = c1;
+    c1 = c2;
   }
   if (errbits) atomicOr(a.err, errbits);
 }
@@ -860,14 +846,16 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
     const int stop = cur.unit == end.unit ? end.sub : a.cls_subtiles[c];
     if (stop > cur.sub) {
       Work wk;
-      wk.job = a.unit_job[cur.unit];
-      wk.njobs = a.unit_njobs[cur.unit];
+      const int unit = __builtin_amdgcn_readfirstlane(cur.unit);  // wave-uniform: scalar loads
+      wk.job = __builtin_amdgcn_readfirstlane(cload(a.unit_job + unit));
+      wk.njobs = cload(a.unit_njobs + unit);
       wk.tok_lo = a.cls_tok_first[c] + cur.sub * kSubTokens;
       wk.tok_hi = min(a.cls_tok_first[c] + stop * kSubTokens, a.cls_tok_first[c] + a.cls_tok_count[c]);
-      const int4 meta = a.jobs[wk.job];
+      const int* mp = reinterpret_cast<const int*>(a.jobs + wk.job);
+      const int meta_y = cload(mp + 1), meta_z = cload(mp + 2);
       const bool two = wk.njobs == 2;
-      if ((meta.y & 0xff) == CB_KIND_K) {
-        if (meta.z & kJobSharedTables) {
+      if ((meta_y & 0xff) == CB_KIND_K) {
+        if (meta_z & kJobSharedTables) {
           if (two) stream_run<D, IO, true, true, 2, 1, POS>(a, lds_w, lds_bias, &lds_next, wk);
           else stream_run<D, IO, true, true, 1, 1, POS>(a, lds_w, lds_bias, &lds_next, wk);
         } else {
