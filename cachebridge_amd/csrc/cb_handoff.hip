@@ -335,14 +335,12 @@ struct MapArgs {
   int32_t total_items;
   int32_t padded_items;
   // Streaming kernel: cost-balanced ranges (one workgroup per CU).
-  const int32_t* unit_cost_prefix;  // [units + 1] prefix sums of per-unit cost weights
   int32_t cls_unit_end[kMaxClasses];
   int32_t cls_subtiles[kMaxClasses];     // 16-token sub-tiles of each class's tokens
-  int64_t cls_cost_begin[kMaxClasses + 1];
   int32_t num_units;
   int32_t num_blocks;
   // Range r of the cost line covers (unit, sub-tile) from blk_unit/sub[r] to
-  // blk_unit/sub[r + 1] (computed on the host with cost_to_pos).
+  // blk_unit/sub[r + 1] (cut on the host, split_cost_line).
   int32_t blk_unit[kMaxStreamBlocks + 1];
   int32_t blk_sub[kMaxStreamBlocks + 1];
   int32_t* err;
@@ -385,36 +383,14 @@ __device__ inline bool decode_work(const MapArgs& a, Work* w) {
   return true;
 }
 
-// Streaming kernel work split. Every (unit, 16-token sub-tile) has a cost
-// weight (the unit's kind and job count); the weights laid end to end, class
-// by class, form one cost line that is cut into num_blocks equal ranges. A
-// cut at cost P falls in sub-tile floor((P - unit start) / weight) of its
-// unit, so neighbouring ranges share the cut and tile the work exactly.
-// Workgroup b takes range (b & 7) * (num_blocks / 8) + (b >> 3): each XCD
-// owns one contiguous eighth of the cost line, so units that read the same
-// source rows (adjacent in the unit order) share that XCD's L2.
+// Streaming kernel work split: workgroup b takes range (b & 7) *
+// (num_blocks / 8) + (b >> 3) of the cost line, so each XCD owns one
+// contiguous eighth of it and units that read the same source rows (adjacent
+// in the unit order) share that XCD's L2.
 struct Pos {
   int unit, sub;
 };
 static_assert(sizeof(MapArgs) <= 4096, "kernel arguments must fit 4 KB");
-
-__host__ __device__ inline Pos cost_to_pos(const MapArgs& a, int64_t P) {
-  if (P >= a.cls_cost_begin[a.ncls]) return Pos{a.num_units, 0};
-  int c = 0;
-  while (c + 1 < a.ncls && P >= a.cls_cost_begin[c + 1]) ++c;
-  const int64_t q = P - a.cls_cost_begin[c];
-  const int64_t ns = a.cls_subtiles[c];
-  const int ub = a.cls_unit_begin[c];
-  const int64_t base = a.unit_cost_prefix[ub];
-  int lo = ub, hi = a.cls_unit_end[c] - 1;  // largest u with (prefix[u] - base) * ns <= q
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if ((a.unit_cost_prefix[mid] - base) * ns <= q) lo = mid;
-    else hi = mid - 1;
-  }
-  const int64_t w = a.unit_cost_prefix[lo + 1] - a.unit_cost_prefix[lo];
-  return Pos{lo, static_cast<int>((q - (a.unit_cost_prefix[lo] - base) * ns) / w)};
-}
 
 // Position of token t of the launch (see MapArgs::pos).
 __device__ inline int position_of(const MapArgs& a, int t) {
@@ -1254,12 +1230,9 @@ struct cb_plan {
   int32_t* d_unit_group = nullptr;
   int32_t* d_group_unit_start = nullptr;
   int32_t* d_group_unit_count = nullptr;
-  int32_t* d_unit_cost_prefix = nullptr;
   int num_units = 0;
   int num_cus = 256;
-  std::vector<int32_t> h_unit_cost_prefix;
-  int64_t cls_unit_weight_begin[kMaxClasses] = {0, 0, 0, 0};  // unit cost prefix at class bounds
-  int64_t cls_unit_weight_end[kMaxClasses] = {0, 0, 0, 0};
+  std::vector<int32_t> unit_weight;  // cost of one 16-token sub-tile of each unit
   float* d_cos = nullptr;
   float* d_sin = nullptr;
   float* d_ucos = nullptr;
@@ -1275,7 +1248,7 @@ void plan_free(cb_plan* p) {
   void* ptrs[] = {p->d_w,         p->d_bias,         p->d_jobs,           p->d_pairs,
                   p->d_unit_job,  p->d_unit_njobs,   p->d_unit_group,     p->d_group_unit_start,
                   p->d_group_unit_count, p->d_cos,   p->d_sin,            p->d_ucos,
-                  p->d_usin,      p->d_err,          p->d_sink,           p->d_unit_cost_prefix};
+                  p->d_usin,      p->d_err,          p->d_sink};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
   delete p;
@@ -1439,22 +1412,15 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   }
   // Relative cost of one 16-token sub-tile of each unit (streaming kernel):
   // a per-kind base (gather; keys also un-rotate and read tables) plus a
-  // per-job part (MFMAs, epilogue, stores). Keys cost ~1.4x values.
-  {
-    std::vector<int32_t> prefix(unit_job.size() + 1, 0);
-    for (size_t u = 0; u < unit_job.size(); ++u) {
-      const int4 m = jobs[unit_job[u]];
-      const bool key = (m.y & 0xff) == CB_KIND_K;
-      int w = (key ? 6 : 2) + 4 * unit_njobs[u];
-      if (key && !(m.z & kJobSharedTables)) w += 2;
-      prefix[u + 1] = prefix[u] + w;
-    }
-    if ((rc = upload(&p->d_unit_cost_prefix, prefix.data(), prefix.size() * 4, &bytes))) return rc;
-    p->h_unit_cost_prefix = prefix;
-    for (int c = 0; c < d->num_windows; ++c) {
-      p->cls_unit_weight_begin[c] = prefix[p->cls_unit_begin[c]];
-      p->cls_unit_weight_end[c] = prefix[p->cls_unit_end[c]];
-    }
+  // per-job part (MFMAs, epilogue, stores). Measured per-CU slopes on MI355X:
+  // a two-job key unit ~49 ns/token, a two-job value unit ~29 ns/token.
+  p->unit_weight.assign(unit_job.size(), 0);
+  for (size_t u = 0; u < unit_job.size(); ++u) {
+    const int4 m = jobs[unit_job[u]];
+    const bool key = (m.y & 0xff) == CB_KIND_K;
+    int w = key ? 7 + 5 * unit_njobs[u] : 2 + 4 * unit_njobs[u];
+    if (key && !(m.z & kJobSharedTables)) w += 2;
+    p->unit_weight[u] = w;
   }
   int32_t* d_order = nullptr;
   CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), order.size() * 4));
@@ -1540,6 +1506,74 @@ void class_ranges(const cb_plan* p, int64_t n, int64_t position_start, int64_t p
   }
 }
 
+// Fixed cost of one segment (a workgroup's pass over part of one unit), in
+// sub-tile weight units: staging the unit's W into LDS, the pipeline ramp and
+// the wait for the slowest wave, about 12 us on MI355X against ~46 ns per
+// weight unit.
+constexpr int64_t kSegmentCost = 256;
+
+// Cut the units' sub-tiles, in order, into a.num_blocks contiguous ranges and
+// store the cut points in a.blk_unit / a.blk_sub. A range costs kSegmentCost
+// per unit it touches plus its sub-tiles' weights; the cuts minimise the
+// largest range cost (greedy fill for a given budget, bisection on the
+// budget), so ranges that cross a unit boundary get fewer sub-tiles.
+void split_cost_line(const cb_plan* p, MapArgs* a) {
+  const int nu = p->num_units, nb = a->num_blocks;
+  std::vector<int32_t> ns(nu, 0);
+  int64_t total = 0;
+  int c = 0;
+  for (int u = 0; u < nu; ++u) {
+    while (c + 1 < p->num_windows && u >= a->cls_unit_end[c]) ++c;
+    ns[u] = a->cls_subtiles[c];
+    if (ns[u] > 0) total += kSegmentCost + static_cast<int64_t>(p->unit_weight[u]) * ns[u];
+  }
+  // Greedy fill with budget T per range; returns the ranges used (cuts into
+  // blk_* when `out`).
+  auto fill = [&](int64_t T, bool out) {
+    int u = 0, sub = 0, r = 0;
+    while (u < nu && ns[u] == 0) ++u;
+    while (u < nu) {
+      if (out) {
+        a->blk_unit[r] = u;
+        a->blk_sub[r] = sub;
+      }
+      int64_t budget = T - kSegmentCost;
+      bool first = true;
+      while (u < nu) {
+        const int64_t w = p->unit_weight[u];
+        int64_t k = std::min<int64_t>(ns[u] - sub, std::max<int64_t>(budget, 0) / w);
+        if (first && k == 0) k = 1;  // every range makes progress
+        first = false;
+        sub += static_cast<int>(k);
+        budget -= k * w;
+        if (sub < ns[u]) break;
+        int nxt = u + 1;
+        while (nxt < nu && ns[nxt] == 0) ++nxt;
+        u = nxt;
+        sub = 0;
+        if (u >= nu || budget < kSegmentCost + p->unit_weight[u]) break;
+        budget -= kSegmentCost;
+      }
+      ++r;
+      if (r > nb && !out) return r;
+    }
+    if (out) {
+      for (int q = r; q <= nb; ++q) {
+        a->blk_unit[q] = nu;
+        a->blk_sub[q] = 0;
+      }
+    }
+    return r;
+  };
+  int64_t lo = 1, hi = total + kSegmentCost;
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    if (fill(mid, false) <= nb) hi = mid;
+    else lo = mid + 1;
+  }
+  fill(lo, true);
+}
+
 // Enqueue the map kernel over class token ranges [first[c], first[c] +
 // count[c]) of the launch's token space. `a` carries the two sides (and, for
 // batches, the position vector); the plan fields are filled in here.
@@ -1591,32 +1625,22 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
   a.padded_items = static_cast<int32_t>((items + 7) / 8 * 8);
   int64_t grid_blocks = a.padded_items;
   if (ws) {
-    // Cost line: class by class, unit weight x sub-tiles of the class.
-    int64_t cost = 0, unit_tokens = 0;
+    int64_t unit_tokens = 0, subtiles = 0;
     for (int c = 0; c < p->num_windows; ++c) {
       const int64_t sub = (static_cast<int64_t>(a.cls_tok_count[c]) + kSubTokens - 1) / kSubTokens;
       a.cls_unit_end[c] = p->cls_unit_end[c];
       a.cls_subtiles[c] = static_cast<int32_t>(sub);
-      a.cls_cost_begin[c] = cost;
-      cost += (p->cls_unit_weight_end[c] - p->cls_unit_weight_begin[c]) * sub;
       unit_tokens += static_cast<int64_t>(p->cls_unit_end[c] - p->cls_unit_begin[c]) * a.cls_tok_count[c];
+      subtiles += sub;
     }
-    a.cls_cost_begin[p->num_windows] = cost;
-    if (cost == 0) return CB_OK;
-    a.unit_cost_prefix = p->d_unit_cost_prefix;
+    if (subtiles == 0) return CB_OK;
     a.num_units = p->num_units;
     int64_t nb = p->num_cus;
     if (tokens_per_workgroup > 0)  // cap on unit-tokens per workgroup
       nb = std::min<int64_t>(nb, std::max<int64_t>(8, (unit_tokens + chunk - 1) / chunk));
     a.num_blocks = static_cast<int32_t>(std::max<int64_t>(8, nb / 8 * 8));
     grid_blocks = a.num_blocks;
-    MapArgs host = a;  // cost_to_pos reads the prefix through the args
-    host.unit_cost_prefix = p->h_unit_cost_prefix.data();
-    for (int r = 0; r <= a.num_blocks; ++r) {
-      const Pos q = cost_to_pos(host, cost * r / a.num_blocks);
-      a.blk_unit[r] = q.unit;
-      a.blk_sub[r] = q.sub;
-    }
+    split_cost_line(p, &a);
   }
   const dim3 grid(static_cast<unsigned>(grid_blocks)), block(ws ? kStreamThreads : kThreads);
   if (ws) {
