@@ -574,16 +574,18 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     }
   };
 
-  // Source dims and un-rotation tables of the next sub-tile of this wave,
-  // requested one sub-tile ahead (a sub-tile is about a microsecond of one
-  // wave's time, which covers the load latency).
-  uint4 xr[CT][2][C::RUN_U4];
+  // Source dims of this wave's sub-tiles are requested two sub-tiles ahead
+  // (slot = k & 1 for its k-th sub-tile; first-touch source rows come from
+  // HBM), un-rotation tables one ahead (they are shared by every key unit and
+  // stay cached).
+  uint4 xr[2][CT][2][C::RUN_U4];
+  bool live_x[2][CT];
   float uc[CT][TG], us[CT][TG];
-  bool live_x[CT];
-  auto prefetch = [&](int sub, const int32_t (&srow)[CT], const int32_t (&prow)[CT]) {
+  auto prefetch_x = [&](auto slot, const int32_t (&srow)[CT]) {
+    constexpr int st = decltype(slot)::value;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      live_x[ct] = srow[ct] >= 0;
+      live_x[st][ct] = srow[ct] >= 0;
       // Rows without a source read row 0 (always valid) and are zeroed on use.
       const int64_t r = srow[ct] >= 0 ? srow[ct] : 0;
       gcptr p = sbase + r * a.src.row_stride_b + g * G * C::BYTES;
@@ -591,8 +593,13 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int u = 0; u < C::RUN_U4; ++u)
-          xr[ct][h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
-      if constexpr (IS_K) {
+          xr[st][ct][h][u] = gload<uint4>(p + (h * HALF + u * C::E16) * C::BYTES);
+    }
+  };
+  auto prefetch_tab = [&](int sub, const int32_t (&prow)[CT]) {
+    if constexpr (IS_K) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
         const int64_t off = static_cast<int64_t>(PV ? prow[ct] : a.position_start + token_of(sub, ct)) * HALF;
         load_tab<G>(ucos + off, g, uc[ct]);
         load_tab<G>(usin + off, g, us[ct]);
@@ -600,37 +607,41 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     }
   };
 
-  // Sub-tiles are claimed in order by each wave: its first two statically
-  // (wave, wave + 8), the rest from a workgroup counter in LDS as the wave
-  // moves along, so faster waves take more of the segment and all waves
-  // finish within about one sub-tile of each other. A claim is made when its
-  // index loads are issued, two sub-tiles ahead of its multiply.
+  // Sub-tiles are claimed in order by each wave: its first three statically
+  // (wave + 8k), the rest from a workgroup counter in LDS as the wave moves
+  // along, so faster waves take more of the segment and all waves finish
+  // within about one sub-tile of each other. A claim is made when its index
+  // loads are issued, three sub-tiles ahead of its multiply.
   constexpr int SW = kStreamWaves;
-  constexpr int kStatic = 2 * SW;
-  int c0 = wave, c1 = wave + SW;  // current and next sub-tile
+  constexpr int kStatic = 3 * SW;
+  int c0 = wave, c1 = wave + SW, c2 = wave + 2 * SW;  // current, next, after-next
   auto claim = [&]() {  // one claim per wave, broadcast to all lanes
     int v = 0;
     if (lane == 0) v = atomicAdd(lds_next, 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
 
-  // Segment start: the first two sub-tiles' rows and the first one's source
+  // Segment start: the first three sub-tiles' rows and the first two's source
   // dims are requested before waiting for the workgroup's previous segment
   // to release LDS, so their latency overlaps that segment's tail.
-  int32_t sr0[CT], tr_a[CT], pr_a[CT];           // rows / positions of the current sub-tile
-  uint2 fs_b[CT], fd_b[CT];                      // index words of the next sub-tile
-  int32_t fp_b[CT];                              // its position words (batched keys)
+  int32_t tr_a[CT], pr_a[CT], tr_b[CT], pr_b[CT];  // rows / positions of the current and next sub-tile
+  uint2 fs_c[CT], fd_c[CT];                        // index words of the sub-tile after next
+  int32_t fp_c[CT];                                // its position words (batched keys)
   {
-    uint2 fs_a[CT], fd_a[CT];
-    int32_t fp_a[CT];
+    uint2 fs_a[CT], fd_a[CT], fs_b[CT], fd_b[CT];
+    int32_t fp_a[CT], fp_b[CT], sr0[CT], sr1[CT];
     fetch_rows(c0, fs_a, fd_a, fp_a);
     fetch_rows(c1, fs_b, fd_b, fp_b);
+    fetch_rows(c2, fs_c, fd_c, fp_c);
     finish_rows(c0, fs_a, fd_a, fp_a, sr0, tr_a, pr_a);
+    finish_rows(c1, fs_b, fd_b, fp_b, sr1, tr_b, pr_b);
+    prefetch_x(std::integral_constant<int, 0>{}, sr0);
+    prefetch_x(std::integral_constant<int, 1>{}, sr1);
+    prefetch_tab(c0, pr_a);
   }
   constexpr int WPER = NJ * C::W_U4 / kStreamThreads;
   static_assert(NJ * C::W_U4 % kStreamThreads == 0 && NJ * D <= kStreamThreads, "staging split");
   const float breg = threadIdx.x < NJ * D ? a.bias[static_cast<size_t>(job) * D + threadIdx.x] : 0.f;
-  prefetch(c0, sr0, pr_a);
   __syncthreads();  // the previous segment no longer reads LDS (nor claims)
   // The unit's W goes straight from memory into LDS (16 bytes per lane, each
   // wave filling 1 KB runs), with no register staging. Waiting for every
@@ -649,10 +660,10 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   if (threadIdx.x == 0) *lds_next = kStatic;
   __syncthreads();  // W, bias and claim counter ready
 
-  // One sub-tile of this wave. Outstanding at its start, oldest first: its
-  // source dims, the next sub-tile's index words, the previous one's stores,
-  // so each wait covers only what it needs.
-  while (c0 < nsub) {
+  // One sub-tile of this wave; the source slot is a compile-time constant
+  // (register arrays indexed at run time would be placed in scratch memory).
+  auto body = [&](auto slot) {
+    constexpr int st = decltype(slot)::value;
     const int sub = c0;
     // W fragments are re-read from LDS every sub-tile: keep the compiler from
     // hoisting them into registers.
@@ -672,8 +683,8 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       float x1[G], x2[G];
 #pragma unroll
       for (int u = 0; u < C::RUN_U4; ++u) {
-        unpack16<IO>(xr[ct][0][u], x1 + u * C::E16);
-        unpack16<IO>(xr[ct][1][u], x2 + u * C::E16);
+        unpack16<IO>(xr[st][ct][0][u], x1 + u * C::E16);
+        unpack16<IO>(xr[st][ct][1][u], x2 + u * C::E16);
       }
       if constexpr (IS_K) {
 #pragma unroll
@@ -691,7 +702,7 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
           }
         }
       }
-      if (!live_x[ct]) {
+      if (!live_x[st][ct]) {
 #pragma unroll
         for (int e = 0; e < G; ++e) x1[e] = x2[e] = 0.f;
       }
@@ -705,20 +716,23 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
           bx[ct][ks][x] = __builtin_bit_cast(bf16x8, make_uint4(tw[x][0], tw[x][1], tw[x][2], tw[x][3]));
       }
     }
-    // The next sub-tile: resolve its rows and request its source dims into
-    // the registers just consumed; claim the one after it and issue its
+    // Next sub-tile's tables; the one after: resolve its rows and request its
+    // source dims into the slot just consumed; claim the next and issue its
     // index loads.
-    int c2;
+    prefetch_tab(c1, pr_b);
+    int c3;
     {
-      int32_t sr1[CT], tr1[CT], pr1[CT];
-      finish_rows(c1, fs_b, fd_b, fp_b, sr1, tr1, pr1);
-      prefetch(c1, sr1, pr1);
-      c2 = claim();
-      fetch_rows(c2, fs_b, fd_b, fp_b);
+      int32_t sr2[CT], tr2[CT], pr2[CT];
+      finish_rows(c2, fs_c, fd_c, fp_c, sr2, tr2, pr2);
+      prefetch_x(slot, sr2);
+      c3 = claim();
+      fetch_rows(c3, fs_c, fd_c, fp_c);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        tr_a[ct] = tr1[ct];
-        pr_a[ct] = pr1[ct];
+        tr_a[ct] = tr_b[ct];
+        pr_a[ct] = pr_b[ct];
+        tr_b[ct] = tr2[ct];
+        pr_b[ct] = pr2[ct];
       }
     }
 
@@ -804,6 +818,12 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     }
     c0 = c1;
     c1 = c2;
+    c2 = c3;
+  };
+  while (c0 < nsub) {
+    body(std::integral_constant<int, 0>{});
+    if (c0 >= nsub) break;
+    body(std::integral_constant<int, 1>{});
   }
   if (errbits) atomicOr(a.err, errbits);
 }
@@ -1412,14 +1432,17 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   }
   // Relative cost of one 16-token sub-tile of each unit (streaming kernel):
   // a per-kind base (gather; keys also un-rotate and read tables) plus a
-  // per-job part (MFMAs, epilogue, stores). Measured per-CU slopes on MI355X:
-  // a two-job key unit ~49 ns/token, a two-job value unit ~29 ns/token.
+  // per-job part (MFMAs, epilogue, stores). A unit that is the only one
+  // reading its source rows fetches all of them from HBM (otherwise another
+  // unit of the group has usually brought them into the MALL first) and runs
+  // ~30% slower per token on MI355X.
   p->unit_weight.assign(unit_job.size(), 0);
   for (size_t u = 0; u < unit_job.size(); ++u) {
     const int4 m = jobs[unit_job[u]];
     const bool key = (m.y & 0xff) == CB_KIND_K;
-    int w = key ? 7 + 5 * unit_njobs[u] : 2 + 4 * unit_njobs[u];
+    int w = (key ? 6 : 2) + 4 * unit_njobs[u];
     if (key && !(m.z & kJobSharedTables)) w += 2;
+    if (group_unit_count[unit_group[u]] == 1) w = (w * 13 + 5) / 10;
     p->unit_weight[u] = w;
   }
   int32_t* d_order = nullptr;
@@ -1508,9 +1531,9 @@ void class_ranges(const cb_plan* p, int64_t n, int64_t position_start, int64_t p
 
 // Fixed cost of one segment (a workgroup's pass over part of one unit), in
 // sub-tile weight units: staging the unit's W into LDS, the pipeline ramp and
-// the wait for the slowest wave, about 12 us on MI355X against ~46 ns per
-// weight unit.
-constexpr int64_t kSegmentCost = 256;
+// the wait for the slowest wave (tuned on MI355X with the TP4-share and
+// whole-model handoffs).
+constexpr int64_t kSegmentCost = 128;
 
 // Cut the units' sub-tiles, in order, into a.num_blocks contiguous ranges and
 // store the cut points in a.blk_unit / a.blk_sub. A range costs kSegmentCost
