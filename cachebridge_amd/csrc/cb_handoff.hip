@@ -167,21 +167,32 @@ __device__ inline void load_f32(const CB_GLOBAL float* p, float* out) {
   }
 }
 
-// Plan RoPE tables keep each half-row of D/2 values permuted as
-// [u][lane group g][4]: value j = g*G + 4u + e (G = D/8) sits at u*16 + g*4 + e,
-// so the four lane groups of one load instruction read 64 contiguous bytes.
-__host__ __device__ inline int tab_index(int half, int j) {
+// Plan RoPE tables are stored in blocks of 16 positions. Lane group g (of
+// four, G = D/8 values each) holds half-row values j = g*G + 4u + e; within a
+// block, the four values (u, g) of the 16 positions are consecutive float4s:
+// value j of position pos sits at (pos/16)*(16*D/2) + (4u + g)*64 + (pos%16)*4
+// + e. One table load of a 16-token sub-tile (16 consecutive positions x 4
+// lane groups) then reads 1 KB of contiguous memory.
+constexpr int kTabBlock = 16;  // positions per table block
+__host__ __device__ inline int64_t tab_offset(int half, int64_t pos, int j) {
   const int G = half / 4;
   const int g = j / G, r = j % G;
-  return (r / 4) * 16 + g * 4 + (r % 4);
+  return (pos / kTabBlock) * (static_cast<int64_t>(half) * kTabBlock) + ((r / 4) * 4 + g) * 64 +
+         (pos % kTabBlock) * 4 + (r % 4);
 }
 
-// Load the G table values of lane group g from one permuted half-row.
+// Float offset of value group (u, g) of position pos (see tab_offset).
 template <int G>
-__device__ inline void load_tab(const CB_GLOBAL float* row, int g, float* out) {
+__device__ inline int64_t tab_chunk(int64_t pos, int u, int g) {
+  return (pos / kTabBlock) * (G * 64) + (4 * u + g) * 64 + (pos % kTabBlock) * 4;
+}
+
+// Load the G table values of lane group g at position pos.
+template <int G>
+__device__ inline void load_tab(const CB_GLOBAL float* tab, int64_t pos, int g, float* out) {
 #pragma unroll
   for (int u = 0; u < G / 4; ++u) {
-    const float4 v = *reinterpret_cast<const CB_GLOBAL float4*>(row + u * 16 + g * 4);
+    const float4 v = *reinterpret_cast<const CB_GLOBAL float4*>(tab + tab_chunk<G>(pos, u, g));
     out[4 * u] = v.x;
     out[4 * u + 1] = v.y;
     out[4 * u + 2] = v.z;
@@ -600,9 +611,9 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     if constexpr (IS_K) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        const int64_t off = static_cast<int64_t>(PV ? prow[ct] : a.position_start + token_of(sub, ct)) * HALF;
-        load_tab<G>(ucos + off, g, uc[ct]);
-        load_tab<G>(usin + off, g, us[ct]);
+        const int64_t pos = PV ? prow[ct] : a.position_start + token_of(sub, ct);
+        load_tab<G>(ucos, pos, g, uc[ct]);
+        load_tab<G>(usin, pos, g, us[ct]);
       }
     }
   };
@@ -794,11 +805,12 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
                 sbuf[e] = ts[ct][8 * hg + e];
               }
             } else {
-              const int64_t off = static_cast<int64_t>(PV ? prow[ct] : a.position_start + token_of(sub, ct)) * HALF;
+              const int64_t pos = PV ? prow[ct] : a.position_start + token_of(sub, ct);
 #pragma unroll
               for (int u = 0; u < 2; ++u) {
-                const float4 cv = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off + (2 * hg + u) * 16 + g * 4);
-                const float4 sv = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off + (2 * hg + u) * 16 + g * 4);
+                const int64_t off = tab_chunk<G>(pos, 2 * hg + u, g);
+                const float4 cv = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
+                const float4 sv = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
                 cbuf[4 * u] = cv.x; cbuf[4 * u + 1] = cv.y; cbuf[4 * u + 2] = cv.z; cbuf[4 * u + 3] = cv.w;
                 sbuf[4 * u] = sv.x; sbuf[4 * u + 1] = sv.y; sbuf[4 * u + 2] = sv.z; sbuf[4 * u + 3] = sv.w;
               }
@@ -962,10 +974,10 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
             unpack16<IO>(gload<uint4>(p + (HALF + g * G + u * C::E16) * T::BYTES), x2 + u * C::E16);
           }
           if constexpr (IS_K) {
-            const int64_t off = static_cast<int64_t>(position_of(a, tok[ct])) * HALF;
+            const int64_t pos = position_of(a, tok[ct]);
             float c[G], s[G];
-            load_tab<G>(ucos + off, g, c);
-            load_tab<G>(usin + off, g, s);
+            load_tab<G>(ucos, pos, g, c);
+            load_tab<G>(usin, pos, g, s);
 #pragma unroll
             for (int e = 0; e < G; ++e) {
               const float k1 = x1[e] * c[e] + x2[e] * s[e];
@@ -1015,9 +1027,9 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
       float o1[G], o2[G];
       float c[G], s[G];
       if constexpr (IS_K) {
-        const int64_t off = static_cast<int64_t>(position_of(a, tok[ct])) * HALF;
-        load_tab<G>(rcos + off, g, c);
-        load_tab<G>(rsin + off, g, s);
+        const int64_t pos = position_of(a, tok[ct]);
+        load_tab<G>(rcos, pos, g, c);
+        load_tab<G>(rsin, pos, g, s);
       }
 #pragma unroll
       for (int rt = 0; rt < RT / 2; ++rt) {
@@ -1104,7 +1116,7 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
 __global__ __launch_bounds__(256) void prepare_tables_kernel(
     const float* __restrict__ c, const float* __restrict__ s, float* __restrict__ rc,
     float* __restrict__ rs, float* __restrict__ uc, float* __restrict__ us, int half,
-    int64_t per_theta, unsigned* __restrict__ norm_dev) {
+    int64_t per_theta, int64_t out_per_theta, unsigned* __restrict__ norm_dev) {
 #pragma clang fp contract(off)
   __shared__ unsigned red[256];
   const int64_t base = static_cast<int64_t>(blockIdx.y) * per_theta;
@@ -1114,8 +1126,7 @@ __global__ __launch_bounds__(256) void prepare_tables_kernel(
     const int64_t i = base + k;
     const float cc = c[i], ss = s[i];
     const float m = fmaxf(cc * cc + ss * ss, 1.17549435e-38f);
-    const int64_t row = i / half;
-    const int64_t o = row * half + tab_index(half, static_cast<int>(i % half));
+    const int64_t o = blockIdx.y * out_per_theta + tab_offset(half, k / half, static_cast<int>(k % half));
     rc[o] = cc;
     rs[o] = ss;
     uc[o] = cc / m;
@@ -1389,7 +1400,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   }
 
   const size_t w_elems = static_cast<size_t>(nj) * S * (D / 16) * (D / 32) * p->ntw * kWave * 8;
-  const size_t table = static_cast<size_t>(d->num_thetas) * d->table_positions * (D / 2);
+  const int64_t padded_positions = (static_cast<int64_t>(d->table_positions) + kTabBlock - 1) / kTabBlock * kTabBlock;
+  const size_t table = static_cast<size_t>(d->num_thetas) * padded_positions * (D / 2);
   int rc;
   if ((rc = upload(&p->d_pairs, pairs.data(), pairs.size() * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_unit_job, unit_job.data(), unit_job.size() * 4, &bytes))) return rc;
@@ -1416,7 +1428,7 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     if (e == hipSuccess) {
       hipLaunchKernelGGL(prepare_tables_kernel, dim3(256, d->num_thetas), dim3(256), 0, 0,
                          d->d_cos, d->d_sin, p->d_cos, p->d_sin, p->d_ucos, p->d_usin, D / 2,
-                         static_cast<int64_t>(d->table_positions) * (D / 2), d_norm);
+                         static_cast<int64_t>(d->table_positions) * (D / 2), padded_positions * (D / 2), d_norm);
       e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipMemcpy(norm.data(), d_norm, norm.size() * sizeof(unsigned), hipMemcpyDeviceToHost);
@@ -1622,7 +1634,7 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
   a.sin_tab = p->d_sin;
   a.ucos_tab = p->d_ucos;
   a.usin_tab = p->d_usin;
-  a.theta_stride = static_cast<int64_t>(p->info.table_positions) * (D / 2);
+  a.theta_stride = (static_cast<int64_t>(p->info.table_positions) + kTabBlock - 1) / kTabBlock * kTabBlock * (D / 2);
   a.support = p->info.support;
   a.chunk = chunk;
   a.err = p->d_err;
