@@ -747,6 +747,16 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       }
     }
 
+    // Store rows of this sub-tile, once per job and column tile (the sink for
+    // tokens without a target row), chosen without branches.
+    gptr dst[NJ][CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int64_t roff = static_cast<int64_t>(max(trow[ct], 0)) * a.tgt.row_stride_b;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) dst[j][ct] = trow[ct] >= 0 ? tbase[j] + roff : sink;
+    }
+
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const uint4* wj = lds_w + j * C::W_U4;
@@ -822,7 +832,7 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
               o2[e] = y2 * cbuf[e] + y1 * sbuf[e];
             }
           }
-          gptr p = trow[ct] >= 0 ? tbase[j] + static_cast<int64_t>(trow[ct]) * a.tgt.row_stride_b : sink;
+          gptr p = dst[j][ct];
           store_elems<IO, 8>(p + (g * G + 8 * hg) * C::BYTES, o1);
           store_elems<IO, 8>(p + (HALF + g * G + 8 * hg) * C::BYTES, o2);
         }
