@@ -499,9 +499,11 @@ struct Gm {
 
 template <int D, typename IO, bool IS_K, bool SHARED, int NJ, int CT, bool POS>
 __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int* lds_next, const Work& wk) {
-  // Separately rounded products and sums (as the reference's torch ops), so
-  // every instantiation rounds identically: a job's rows are bit-identical
-  // whichever unit shape or plan computes them.
+  // No implicit contraction: every fused multiply-add is written out, so every
+  // instantiation rounds identically and a job's rows are bit-identical
+  // whichever unit shape or plan computes them. (The rotations use explicit
+  // FMAs; the reference's separately rounded fp32 ops differ from them by at
+  // most one fp32 rounding, far below the bf16 result's.)
 #pragma clang fp contract(off)
   using C = Gm<D, IO>;
   using T = IOTraits<IO>;
@@ -700,8 +702,8 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       if constexpr (IS_K) {
 #pragma unroll
         for (int e = 0; e < G; ++e) {
-          const float k1 = x1[e] * uc[ct][e] + x2[e] * us[ct][e];
-          const float k2 = x2[e] * uc[ct][e] - x1[e] * us[ct][e];
+          const float k1 = __builtin_fmaf(x1[e], uc[ct][e], x2[e] * us[ct][e]);
+          const float k2 = __builtin_fmaf(x2[e], uc[ct][e], -(x1[e] * us[ct][e]));
           x1[e] = k1;
           x2[e] = k2;
         }
@@ -828,8 +830,8 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
               const float y1 = o1[e], y2 = o2[e];
-              o1[e] = y1 * cbuf[e] - y2 * sbuf[e];
-              o2[e] = y2 * cbuf[e] + y1 * sbuf[e];
+              o1[e] = __builtin_fmaf(y1, cbuf[e], -(y2 * sbuf[e]));
+              o2[e] = __builtin_fmaf(y2, cbuf[e], y1 * sbuf[e]);
             }
           }
           gptr p = dst[j][ct];
@@ -990,8 +992,8 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
             load_tab<G>(usin, pos, g, s);
 #pragma unroll
             for (int e = 0; e < G; ++e) {
-              const float k1 = x1[e] * c[e] + x2[e] * s[e];
-              const float k2 = x2[e] * c[e] - x1[e] * s[e];
+              const float k1 = __builtin_fmaf(x1[e], c[e], x2[e] * s[e]);
+              const float k2 = __builtin_fmaf(x2[e], c[e], -(x1[e] * s[e]));
               x1[e] = k1;
               x2[e] = k2;
             }
@@ -1049,8 +1051,8 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
           const float y1 = acc[rt][ct][i] + bias1[e];
           const float y2 = acc[rt + RT / 2][ct][i] + bias2[e];
           if constexpr (IS_K) {
-            o1[e] = y1 * c[e] - y2 * s[e];
-            o2[e] = y2 * c[e] + y1 * s[e];
+            o1[e] = __builtin_fmaf(y1, c[e], -(y2 * s[e]));
+            o2[e] = __builtin_fmaf(y2, c[e], y1 * s[e]);
           } else {
             o1[e] = y1;
             o2[e] = y2;
