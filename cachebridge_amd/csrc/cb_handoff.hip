@@ -92,6 +92,9 @@ __device__ inline gcptr as_global(const void* p) { return (gcptr)p; }
 __device__ inline gptr as_global(void* p) { return (gptr)p; }
 __device__ inline const CB_GLOBAL float* gtab(const float* p) { return (const CB_GLOBAL float*)p; }
 
+// Cache-policy operand of the LDS-DMA builtin: the non-temporal bit.
+constexpr int kCachePolicyNT = 2;
+
 constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
@@ -356,6 +359,7 @@ struct MapArgs {
   int32_t blk_sub[kMaxStreamBlocks + 1];
   int32_t* err;
   void* sink;  // scratch destination of stores without a target row
+  const void* zero;  // one all-zero head row: the gather source of tokens without a source row
   // Batched launches: position of every token (tokens then index resolved
   // rows: src/tgt are int32 row vectors over the same token space). Null for
   // one request, whose token t sits at position_start + t.
@@ -462,6 +466,7 @@ constexpr int kStreamWaves = 8;
 constexpr int kStreamThreads = kWave * kStreamWaves;
 constexpr int kSubTokens = 16;                   // tokens per wave sub-tile
 constexpr int kSinkBytes = kWave * 128 * 4;       // one head row (D <= 128, fp32) per lane
+constexpr int kZeroBytes = 128 * 4;               // one zero head row, after the sink
 
 __host__ __device__ inline int gen_out_dim(int D, int rt, int r) {
   const int per_half = D / 32;
@@ -592,16 +597,15 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   // HBM), un-rotation tables one ahead (they are shared by every key unit and
   // stay cached).
   uint4 xr[2][CT][2][C::RUN_U4];
-  bool live_x[2][CT];
   float uc[CT][TG], us[CT][TG];
+  gcptr zrow = as_global(a.zero);
   auto prefetch_x = [&](auto slot, const int32_t (&srow)[CT]) {
     constexpr int st = decltype(slot)::value;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      live_x[st][ct] = srow[ct] >= 0;
-      // Rows without a source read row 0 (always valid) and are zeroed on use.
-      const int64_t r = srow[ct] >= 0 ? srow[ct] : 0;
-      gcptr p = sbase + r * a.src.row_stride_b + g * G * C::BYTES;
+      // Tokens without a source row gather the plan's zero row.
+      gcptr p = (srow[ct] >= 0 ? sbase + static_cast<int64_t>(srow[ct]) * a.src.row_stride_b : zrow) +
+                g * G * C::BYTES;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -659,14 +663,17 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   // The unit's W goes straight from memory into LDS (16 bytes per lane, each
   // wave filling 1 KB runs), with no register staging. Waiting for every
   // older load here costs little: W is the last thing requested, and the
-  // loop then starts with nothing outstanding.
+  // loop then starts with nothing outstanding. The loads are non-temporal
+  // (W is read once per segment), which leaves L2 to the source rows and
+  // RoPE tables.
   {
     gcptr wsrc = as_global(a.w + static_cast<size_t>(job) * C::W_U4);
     const int wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
     for (int i = 0; i < WPER; ++i)
       __builtin_amdgcn_global_load_lds(wsrc + (i * kStreamThreads + threadIdx.x) * 16,
-                                       (CB_LDS void*)(lds_w + i * kStreamThreads + wv * kWave), 16, 0, 0);
+                                       (CB_LDS void*)(lds_w + i * kStreamThreads + wv * kWave), 16, 0,
+                                       kCachePolicyNT);
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
   }
   if (threadIdx.x < NJ * D) lds_bias[threadIdx.x] = breg;
@@ -689,10 +696,19 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
     }
 
     // Un-rotate (keys) and split the current sub-tile into B fragments.
+    // Values stored as bf16 are their own single term: the loaded 16 bytes
+    // (8 consecutive dims of one half) are the fragment of k-step ks.
     bf16x8 bx[CT][KS][XT];
     float tc[CT][SHARED ? G : 1], ts[CT][SHARED ? G : 1];
+    constexpr bool RAW = !IS_K && XT == 1 && C::BYTES == 2;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
+      if constexpr (RAW) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          bx[ct][ks][0] = __builtin_bit_cast(bf16x8, xr[st][ct][ks / (KS / 2)][ks % (KS / 2)]);
+        continue;
+      }
       float x1[G], x2[G];
 #pragma unroll
       for (int u = 0; u < C::RUN_U4; ++u) {
@@ -714,10 +730,6 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
             ts[ct][e] = us[ct][e];
           }
         }
-      }
-      if (!live_x[st][ct]) {
-#pragma unroll
-        for (int e = 0; e < G; ++e) x1[e] = x2[e] = 0.f;
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -766,12 +778,13 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       for (int hg = 0; hg < NGRP; ++hg) {
         // Row tiles of this group: 2hg, 2hg+1 and their partners.
         auto tile = [&](int q) { return 2 * hg + (q & 1) + (q >> 1) * (RT / 2); };
-        f32x4 acc[4][CT];
+        // The bias of each row tile is the accumulator input of its first
+        // product (no register copies per column tile).
+        f32x4 acc[4][CT], bq[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float* b = lds_bias + j * D + gen_out_dim(D, tile(q), 4 * g);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct) acc[q][ct] = f32x4{b[0], b[1], b[2], b[3]};
+          bq[q] = f32x4{b[0], b[1], b[2], b[3]};
         }
         // W fragments flow through a three-slot ring, read two steps ahead;
         // each fragment feeds the CT column tiles.
@@ -790,9 +803,14 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
             if (t + 2 < NSTEP) read_w(t + 2, ring[(t + 2) % 3]);
             const int ks = t % KS, q = t / KS;
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
-              for_products<XT, NTW>(
-                  [&](int ii, int jj) { acc[q][ct] = mfma(ring[t % 3][jj], bx[ct][ks][ii], acc[q][ct]); });
+            for (int ct = 0; ct < CT; ++ct) {
+              int pi = 0;
+              for_products<XT, NTW>([&](int ii, int jj) {
+                const f32x4 c = ks == 0 && pi == 0 ? bq[q] : acc[q][ct];
+                acc[q][ct] = mfma(ring[t % 3][jj], bx[ct][ks][ii], c);
+                ++pi;
+              });
+            }
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -1428,8 +1446,9 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   if ((rc = upload(&p->d_ucos, nullptr, table * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_usin, nullptr, table * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_err, nullptr, 4, &bytes))) return rc;
-  if ((rc = upload(&p->d_sink, nullptr, kSinkBytes, &bytes))) return rc;
+  if ((rc = upload(&p->d_sink, nullptr, kSinkBytes + kZeroBytes, &bytes))) return rc;
   CB_HIP(hipMemset(p->d_err, 0, 4));
+  CB_HIP(hipMemset(static_cast<char*>(p->d_sink) + kSinkBytes, 0, kZeroBytes));
   // Rotation / un-rotation tables in the permuted layout, and which theta sets
   // have unit norm (|cos^2 + sin^2 - 1| <= 2 ulp) so keys can share one table.
   {
@@ -1651,6 +1670,7 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
   a.chunk = chunk;
   a.err = p->d_err;
   a.sink = p->d_sink;
+  a.zero = static_cast<const char*>(p->d_sink) + kSinkBytes;
   int64_t items = 0, n_total = 0;
   a.ncls = p->num_windows;
   for (int c = 0; c < p->num_windows; ++c) {
