@@ -525,7 +525,8 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
   constexpr bool PV = POS && IS_K;
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  // Wave-uniform (scalar), so sub-tile indices and the loop stay uniform.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane >> 4;
   const int col = lane & 15;
 
