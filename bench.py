@@ -251,6 +251,7 @@ def main() -> int:
             "tokens_per_s": round(ns.tokens / (kms_n * 1e-3), 1),
             "hbm_frac": round(b / (kms_n * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_launch": b,
+            "traffic": profiled_traffic("map_install_stream", "full"),
         }
         del hn
         torch.cuda.empty_cache()
