@@ -168,6 +168,57 @@ def copy_calibration(mib: int = 1024, steps: int = 5) -> None:
     print(json.dumps({"copy_calibration_mib": mib, "launches": steps}), flush=True)
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3
+DELTA_STATE = dict(layers=48, heads=32, dim=128)
+
+
+def delta_state_bench(steps: int, warmup: int) -> dict:
+    """Recurrent-state transform A^T U B of a Qwen3.5-style hybrid model: one
+    fp32 [128, 128] state per (linear-attention layer, value head) with its own
+    key and value bases, all in one launch of cb_delta_state_transform."""
+    import torch
+
+    from cachebridge_amd import architectures
+
+    n = DELTA_STATE["layers"] * DELTA_STATE["heads"]
+    d = DELTA_STATE["dim"]
+    g = torch.Generator(device="cuda").manual_seed(5)
+    u = torch.randn(n, d, d, device="cuda", generator=g)
+    a = torch.randn(n, d, d, device="cuda", generator=g) / d ** 0.5
+    b = torch.randn(n, d, d, device="cuda", generator=g) / d ** 0.5
+    for _ in range(warmup):
+        architectures.transform_delta_state(u, a, b)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        architectures.transform_delta_state(u, a, b)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = statistics.fmean(s.elapsed_time(e) for s, e in zip(starts, ends))
+    flops = n * 2 * 2 * d ** 3
+    bytes_alg = n * 4 * d * d * 4
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    return {
+        "metric": "recurrent-state transforms/s (A^T U B, fp32 128x128, Qwen3.5-style 48 layers x 32 heads)",
+        "value": round(steps * n / wall, 1), "unit": "matrices/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(wall / steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,1) states, "
+        "N(0,1/128) bases)",
+        "config": {"workload": f"{n} recurrent states [{d}x{d}] fp32 with per-state bases", **DELTA_STATE},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "delta_state128_kernel (fp32, 128x128)", "algorithmic_flops_per_launch": flops,
+                     "algorithmic_bytes_per_launch": bytes_alg,
+                     "hbm_gbs": round(bytes_alg / (kernel_ms * 1e-3) / 1e9, 1),
+                     "kernel_ms_mean": round(kernel_ms, 5)},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -181,9 +232,14 @@ def main() -> int:
     ap.add_argument("--tokens-per-workgroup", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
+    ap.add_argument("--delta-state", action="store_true",
+                    help="only time the recurrent-state transform (Qwen3.5-style hybrid model)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return 0
+    if args.delta_state:
+        print(json.dumps(delta_state_bench(args.steps, args.warmup)), flush=True)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the handoff "

@@ -22,6 +22,7 @@ CB_ENOMEM = -12
 CB_EHIP = -5
 CB_DTYPE_BF16 = 0
 CB_DTYPE_F32 = 1
+CB_DTYPE_F64 = 2
 CB_KIND_K = 0
 CB_KIND_V = 1
 CB_INDEX_IDENTITY = 0
@@ -141,6 +142,11 @@ SIGNATURES = {
         [ctypes.POINTER(CbRows), ctypes.POINTER(CbRows), _i32, _i32, _i32, _i32, _c_void_p, _c_void_p],
     ),
     "cb_plan_read_errors": (ctypes.c_int, [_c_void_p, ctypes.POINTER(_i32), _c_void_p]),
+    "cb_delta_state_transform": (
+        ctypes.c_int,
+        [_i32, _i64, _i32, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
+         _c_void_p, _i64, _c_void_p],
+    ),
 }
 
 _LIB: ctypes.CDLL | None = None

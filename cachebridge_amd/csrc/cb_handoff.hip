@@ -1214,6 +1214,192 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(CopyArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Recurrent (DeltaNet) state transform: out[b] = A[b]^T . U[b] . B[b]
+// (cb/architectures/qwen35.py:52-61) with U [k, v], A [k, kp], B [v, vp],
+// out [kp, vp], row-major fp32 or fp64. One workgroup per (batch entry,
+// 16-row block of out): stage 1 forms the block's 16 rows of T = A^T U in LDS,
+// stage 2 multiplies them by B. Both stages are 16x16x4 MFMAs (lane l holds
+// A[l % 16][l / 16] and B[l / 16][l % 16]; the result rows 4(l / 16) + j of
+// column l % 16), with operands outside the matrices read as zero.
+// ---------------------------------------------------------------------------
+
+constexpr int kDeltaMaxV = 512;  // LDS holds 16 rows of T (16 x v, fp64)
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct DeltaMfma;
+template <>
+struct DeltaMfma<float> {
+  using V = f32x4;
+  static __device__ inline V op(float a, float b, V c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+};
+template <>
+struct DeltaMfma<double> {
+  using V = f64x4;
+  static __device__ inline V op(double a, double b, V c) { return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0); }
+};
+
+struct DeltaArgs {
+  const void* u;
+  const void* a;
+  const void* b;
+  void* out;
+  int64_t su, sa, sb, so;  // batch strides in elements (0: one matrix for every entry)
+  int32_t k, v, kp, vp;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void delta_state_kernel(DeltaArgs p) {
+  __shared__ double tblk_raw[16 * kDeltaMaxV];
+  T* tblk = reinterpret_cast<T*>(tblk_raw);
+  using M = DeltaMfma<T>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t bi = blockIdx.x;
+  const int i0 = blockIdx.y * 16;
+  const T* U = static_cast<const T*>(p.u) + bi * p.su;
+  const T* A = static_cast<const T*>(p.a) + bi * p.sa;
+  const T* B = static_cast<const T*>(p.b) + bi * p.sb;
+  T* out = static_cast<T*>(p.out) + bi * p.so;
+  // Stage 1: T[i0 + row][c] = sum_k A[k][i0 + row] * U[k][c] for the block's 16 rows.
+  for (int c0 = wave * 16; c0 < p.v; c0 += 64) {
+    typename M::V acc = {0, 0, 0, 0};
+    const int ia = i0 + r, cu = c0 + r;
+#pragma unroll 4
+    for (int kk = 0; kk < p.k; kk += 4) {
+      const int kr = kk + q;
+      const T av = kr < p.k && ia < p.kp ? A[static_cast<int64_t>(kr) * p.kp + ia] : T(0);
+      const T bv = kr < p.k && cu < p.v ? U[static_cast<int64_t>(kr) * p.v + cu] : T(0);
+      acc = M::op(av, bv, acc);
+    }
+    if (cu < p.v) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tblk[(4 * q + j) * p.v + cu] = acc[j];
+    }
+  }
+  __syncthreads();
+  // Stage 2: out[i0 + row][c] = sum_v T[row][v] * B[v][c].
+  for (int c0 = wave * 16; c0 < p.vp; c0 += 64) {
+    typename M::V acc = {0, 0, 0, 0};
+    const int cb = c0 + r;
+#pragma unroll 4
+    for (int vv = 0; vv < p.v; vv += 4) {
+      const int vr = vv + q;
+      const T av = vr < p.v ? tblk[r * p.v + vr] : T(0);
+      const T bv = vr < p.v && cb < p.vp ? B[static_cast<int64_t>(vr) * p.vp + cb] : T(0);
+      acc = M::op(av, bv, acc);
+    }
+    if (cb < p.vp) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = i0 + 4 * q + j;
+        if (row < p.kp) out[static_cast<int64_t>(row) * p.vp + cb] = acc[j];
+      }
+    }
+  }
+}
+
+// fp32 states with every dimension 128 (the DeltaNet head size): one
+// workgroup of 8 waves per batch entry, two workgroups per CU. Wave w owns
+// the 16 rows [16w, 16w + 16) of T and of out.
+//   Stage 1 forms T^T = U^T A as eight 16x16 tiles (v-block vb, row block w):
+//   A operand U[k][16vb + r], B operand A[k][16w + r], over four 32-row
+//   chunks of A and U staged through LDS (double-buffered; the next chunk's
+//   loads are in flight during the current chunk's MFMAs).
+//   Stage 2 uses those accumulators directly as the A operand of out = T B:
+//   lane (q, r) of tile vb holds T[16w + r][16vb + 4q + e], so k-step (vb, e)
+//   pairs lane q with row 16vb + 4q + e of B (a permuted k order; the sum over
+//   v is the same). B streams through the same LDS buffers.
+// Chunk rows are padded to 144 floats, so every operand read of a k-step hits
+// 64 distinct banks.
+constexpr int kDs = 128;        // matrix size of the fast path
+constexpr int kDsChunk = 32;    // rows per staged chunk
+constexpr int kDsPadC = 144;    // chunk row stride (floats)
+constexpr int kDsChunkFloats = kDsChunk * kDsPadC;
+
+__global__ __launch_bounds__(512, 2) void delta_state128_kernel(DeltaArgs p) {
+  __shared__ float lds[4 * kDsChunkFloats];  // stage 1: A0 U0 A1 U1; stage 2: B0 B1
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t bi = blockIdx.x;
+  const float* U = static_cast<const float*>(p.u) + bi * p.su;
+  const float* A = static_cast<const float*>(p.a) + bi * p.sa;
+  const float* B = static_cast<const float*>(p.b) + bi * p.sb;
+  float* out = static_cast<float*>(p.out) + bi * p.so;
+  // Chunk staging: thread t moves 16 bytes of rows t / 32 and t / 32 + 16.
+  const int srow = threadIdx.x >> 5, scol = (threadIdx.x & 31) * 4;
+  auto load_chunk = [&](const float* m, int c, float4& v0, float4& v1) {
+    v0 = *reinterpret_cast<const float4*>(m + (c * kDsChunk + srow) * kDs + scol);
+    v1 = *reinterpret_cast<const float4*>(m + (c * kDsChunk + srow + 16) * kDs + scol);
+  };
+  auto store_chunk = [&](float* dst, const float4& v0, const float4& v1) {
+    *reinterpret_cast<float4*>(dst + srow * kDsPadC + scol) = v0;
+    *reinterpret_cast<float4*>(dst + (srow + 16) * kDsPadC + scol) = v1;
+  };
+  constexpr int NC = kDs / kDsChunk;
+  constexpr int NB = kDs / 16;
+
+  // Stage 1: tt[vb] = (U^T A) tile (vb, w), i.e. T[16w + r][16vb + 4q + e].
+  f32x4 tt[NB];
+#pragma unroll
+  for (int vb = 0; vb < NB; ++vb) tt[vb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float4 a0, a1, u0, u1, b0, b1;
+  load_chunk(A, 0, a0, a1);
+  load_chunk(U, 0, u0, u1);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float* bufA = lds + (c & 1) * 2 * kDsChunkFloats;
+    float* bufU = bufA + kDsChunkFloats;
+    store_chunk(bufA, a0, a1);
+    store_chunk(bufU, u0, u1);
+    __syncthreads();
+    if (c + 1 < NC) {
+      load_chunk(A, c + 1, a0, a1);
+      load_chunk(U, c + 1, u0, u1);
+    } else {
+      load_chunk(B, 0, b0, b1);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kDsChunk; kk += 4) {
+      const float bv = bufA[(kk + q) * kDsPadC + 16 * w + r];
+#pragma unroll
+      for (int vb = 0; vb < NB; ++vb)
+        tt[vb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bufU[(kk + q) * kDsPadC + 16 * vb + r], bv, tt[vb], 0, 0, 0);
+    }
+  }
+
+  // Stage 2: oo[jb] = out tile (w, jb) = sum over v of T[16w + .][v] B[v][16jb + .].
+  f32x4 oo[NB];
+#pragma unroll
+  for (int jb = 0; jb < NB; ++jb) oo[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float* bufB = lds + (c & 1) * kDsChunkFloats;
+    __syncthreads();  // the buffer's previous readers (stage 1, or chunk c - 2) are done
+    store_chunk(bufB, b0, b1);
+    __syncthreads();
+    if (c + 1 < NC) load_chunk(B, c + 1, b0, b1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {        // v-blocks 2c, 2c + 1 of this chunk
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int vrow = 16 * h + 4 * q + e;
+        const float av = tt[2 * c + h][e];  // c and h are unrolled constants
+#pragma unroll
+        for (int jb = 0; jb < NB; ++jb)
+          oo[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bufB[vrow * kDsPadC + 16 * jb + r], oo[jb], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int jb = 0; jb < NB; ++jb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[(16 * w + 4 * q + e) * kDs + 16 * jb + r] = oo[jb][e];
+}
+
+// ---------------------------------------------------------------------------
 // Batched launches: every kept token of every request gets a slot in one
 // token space, class by class (class c's kept tokens of request r occupy
 // [vbase, vbase + count)). This kernel resolves each slot's source row,
@@ -2050,6 +2236,36 @@ int cb_plan_read_errors(cb_plan* p, int32_t* flags, void* stream) {
   CB_HIP(hipStreamSynchronize(s));
   CB_HIP(hipMemsetAsync(p->d_err, 0, 4, s));
   CB_HIP(hipStreamSynchronize(s));
+  return CB_OK;
+}
+
+int cb_delta_state_transform(int32_t dtype, int64_t batch, int32_t k, int32_t v, int32_t kp, int32_t vp,
+                             const void* d_state, int64_t state_stride, const void* d_key_basis,
+                             int64_t key_stride, const void* d_value_basis, int64_t value_stride,
+                             void* d_out, int64_t out_stride, void* stream) {
+  if (dtype != CB_DTYPE_F32 && dtype != CB_DTYPE_F64) return fail(CB_EINVAL, "delta state dtype must be fp32 or fp64");
+  if (batch < 0) return fail(CB_EINVAL, "negative batch");
+  if (k < 1 || v < 1 || kp < 1 || vp < 1) return fail(CB_EINVAL, "matrix dimensions must be positive");
+  if (v > kDeltaMaxV) return fail(CB_EINVAL, "value dimension above %d", kDeltaMaxV);
+  if (state_stride < 0 || key_stride < 0 || value_stride < 0 || out_stride < 0)
+    return fail(CB_EINVAL, "negative batch stride");
+  if (batch == 0) return CB_OK;
+  if (!d_state || !d_key_basis || !d_value_basis || !d_out) return fail(CB_EINVAL, "null matrix pointer");
+  if (out_stride < static_cast<int64_t>(kp) * vp && batch > 1)
+    return fail(CB_EINVAL, "output batch stride overlaps entries");
+  if (batch > 0x7fffffff) return fail(CB_EINVAL, "batch too large");
+  DeltaArgs a{d_state, d_key_basis, d_value_basis, d_out, state_stride, key_stride, value_stride, out_stride,
+              k, v, kp, vp};
+  const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((kp + 15) / 16));
+  const bool square128 = k == kDs && v == kDs && kp == kDs && vp == kDs;
+  if (dtype == CB_DTYPE_F32 && square128)
+    hipLaunchKernelGGL(delta_state128_kernel, dim3(static_cast<unsigned>(batch)), dim3(512), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else if (dtype == CB_DTYPE_F32)
+    hipLaunchKernelGGL(delta_state_kernel<float>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(delta_state_kernel<double>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  CB_HIP(hipGetLastError());
   return CB_OK;
 }
 

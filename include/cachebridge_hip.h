@@ -32,6 +32,8 @@
  *                         (rt/source_mapper_adapter.py:366-428).
  *                         With an identity target index it is map_page's
  *                         dense [2, Lt, n, Ht, D] output (cb/mapper.py:216-239).
+ *   cb_delta_state_transform <- qwen35.transform_delta_state
+ *                         (cb/architectures/qwen35.py:52-61).
  *   cb_copy_rows       <- pack_source_block (cb/online/blocks.py:47-82) and the
  *                         per-run install copies of _DirectMappedPoolCodec.copy
  *                         (rt/source_mapper_adapter.py:400-420).
@@ -55,6 +57,7 @@ extern "C" {
 /* Element type of pages, pools and outputs. */
 #define CB_DTYPE_BF16 0
 #define CB_DTYPE_F32 1
+#define CB_DTYPE_F64 2 /* cb_delta_state_transform only */
 
 /* Job kinds. */
 #define CB_KIND_K 0
@@ -217,6 +220,19 @@ int cb_map_install_batch(const cb_plan* plan, const cb_rows* source, const cb_ro
 int cb_copy_rows(const cb_rows* src, const cb_rows* dst, int32_t num_layers,
                  int32_t num_tokens, int32_t row_elements, int32_t dtype,
                  int32_t* d_error_flag, void* stream);
+
+/* Recurrent-state transform of a linear-attention (DeltaNet) layer:
+   out[b] = A[b]^T . U[b] . B[b] for b in [0, batch), with U the source state
+   [k, v], A the key basis [k, kp], B the value basis [v, vp] and out [kp, vp],
+   all row-major device matrices of dtype CB_DTYPE_F32 or CB_DTYPE_F64. Entry
+   b of each operand starts b * stride elements after its pointer (stride 0
+   uses one matrix for every entry). v <= 512. Asynchronous.
+   Replaces qwen35.transform_delta_state (cb/architectures/qwen35.py:52-61),
+   key_basis^T @ source_state @ value_basis over the batch dimensions. */
+int cb_delta_state_transform(int32_t dtype, int64_t batch, int32_t k, int32_t v, int32_t kp, int32_t vp,
+                             const void* d_state, int64_t state_stride, const void* d_key_basis,
+                             int64_t key_stride, const void* d_value_basis, int64_t value_stride,
+                             void* d_out, int64_t out_stride, void* stream);
 
 /* Read and clear the plan's device error word (bit 0: source row out of
    range, bit 1: target row out of range). Synchronizes `stream`. */

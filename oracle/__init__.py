@@ -20,6 +20,8 @@ reference repository root; ``cb/`` = ``src/cachebridge/``):
   ``MHATokenToKVPool.set_kv_buffer`` (SGLang v0.4.10.post2, un-vendored),
   the virtual-page construction for per-(layer, head) source assignments,
   and ``cb/architectures/gemma3.py:39-58`` window materialisation.
+- ``oracle.structured`` -- ``cb/architectures/qwen35.py:52-61``
+  (``transform_delta_state``), in float64 numpy.
 
 Parity status of each function is stated in its docstring; "parity pinned"
 names the golden vectors or closed forms that check it in ``tests/``.
