@@ -219,6 +219,73 @@ def delta_state_bench(steps: int, warmup: int) -> dict:
     }
 
 
+def delivery_bench(steps: int, warmup: int) -> dict:
+    """Receiver-side delivery of the TP4 share's selected source layers in
+    2048-token blocks (two slots), timed per block; and the whole block-wise
+    handoff (deliver, then map, per block, on one stream) against the fused
+    map from the pool."""
+    import torch
+
+    from cachebridge_amd import synthetic
+    from cachebridge_amd.online.delivery import SelectedBlockDelivery, map_install_delivered
+
+    sh = synthetic.shape("tp4")
+    h = synthetic.make_handoff(sh)
+    block = 2048
+    d = SelectedBlockDelivery(h.source_pool, h.source_slots, layers=h.mapper.source_layers, block_tokens=block)
+    compute = torch.cuda.current_stream()
+    spans = [(a, min(a + block, sh.tokens)) for a in range(0, sh.tokens, block)]
+
+    def pipelined():
+        for i, (a, b) in enumerate(spans):
+            d.deliver(i % 2, a, b)
+            map_install_delivered(h.mapper, d, i % 2, h.target_pool, block_table=h.block_table, page_size=16,
+                                  prefix_length=sh.tokens, stream=compute)
+
+    for _ in range(warmup):
+        pipelined()
+    torch.cuda.synchronize()
+    # delivery kernel alone: one block per step, events on the delivery stream
+    times = []
+    for i in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(d.stream)
+        d.deliver(i % 2, 0, block)
+        e1.record(d.stream)
+        d.release(i % 2, d.stream)
+        times.append((e0, e1))
+    torch.cuda.synchronize()
+    deliver_ms = statistics.fmean(a.elapsed_time(b) for a, b in times)
+    moved = 2 * 2 * len(d.layers) * block * sh.source_heads * sh.head_dim * 2  # read + write
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(compute)
+    for _ in range(steps):
+        pipelined()
+    e1.record(compute)
+    torch.cuda.synchronize()
+    pipe_ms = e0.elapsed_time(e1) / steps
+    e0.record(compute)
+    for _ in range(steps):
+        h.run()
+    e1.record(compute)
+    torch.cuda.synchronize()
+    fused_ms = e0.elapsed_time(e1) / steps
+    gbs = moved / (deliver_ms * 1e-3) / 1e9
+    return {
+        "metric": "selected-layer block delivery (receiver slot fill) GB/s, TP4 share, 2048-token blocks",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": WORKLOADS["tp4"], "block_tokens": block, "delivered_layers": len(d.layers),
+                   "source_layers": sh.source_layers},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "copy_rows_kernel",
+                     "bytes_per_block": moved, "kernel_ms_mean": round(deliver_ms, 5)},
+        "delivered_bytes_per_handoff": 2 * len(d.layers) * sh.tokens * sh.source_heads * sh.head_dim * 2,
+        "all_layer_bytes_per_handoff": 2 * sh.source_layers * sh.tokens * sh.source_heads * sh.head_dim * 2,
+        "delivered_handoff_ms": round(pipe_ms, 4), "fused_handoff_ms": round(fused_ms, 4),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -232,6 +299,8 @@ def main() -> int:
     ap.add_argument("--tokens-per-workgroup", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-north-star", action="store_true")
+    ap.add_argument("--delivery", action="store_true",
+                    help="only time the selected-layer block delivery (receiver slots) at the TP4 share")
     ap.add_argument("--delta-state", action="store_true",
                     help="only time the recurrent-state transform (Qwen3.5-style hybrid model)")
     args = ap.parse_args()
@@ -240,6 +309,9 @@ def main() -> int:
         return 0
     if args.delta_state:
         print(json.dumps(delta_state_bench(args.steps, args.warmup)), flush=True)
+        return 0
+    if args.delivery:
+        print(json.dumps(delivery_bench(args.steps, args.warmup)), flush=True)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the handoff "

@@ -124,12 +124,18 @@ class HeadwiseMapper:
         self._target_layers = lt
         self._max_source_layer = int(al.max())
         self._source_heads = (int(ah.min()), int(ah.max()))
+        self._source_layers = tuple(sorted({int(x) for x in al.flatten().tolist()}))
 
     @classmethod
     def from_assignment(cls, **kwargs) -> "HeadwiseMapper":
         self = cls.__new__(cls)
         self._init_plan(**kwargs)
         return self
+
+    @property
+    def source_layers(self) -> tuple:
+        """Source layers any job reads (the layers a receiver must be sent)."""
+        return self._source_layers
 
     @property
     def target_layers(self) -> int:

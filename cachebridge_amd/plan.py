@@ -111,6 +111,10 @@ def rows_from_layers(k_layers: Sequence[torch.Tensor], v_layers: Sequence[torch.
     if ptrs is None:
         host = torch.tensor(key, dtype=torch.int64)
         ptrs = host.to(first.device)
+        # The table may be read by a kernel on another stream: let the upload
+        # land first (once per table; tables are cached by their pointers).
+        if first.device.type == "cuda":
+            torch.cuda.current_stream(first.device).synchronize()
         if pointer_cache is not None:
             pointer_cache.clear()
             pointer_cache[key] = ptrs
