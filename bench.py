@@ -286,6 +286,97 @@ def delivery_bench(steps: int, warmup: int) -> dict:
     }
 
 
+def cohort_bench(steps: int, warmup: int) -> dict:
+    """An admitted cohort (the first requests of the seeded 64-request length
+    distribution, TP4 share) through the admission state machine: one
+    synchronous map+install transaction per request, FIFO, against the whole
+    cohort mapped in one launch and then published FIFO. Wall-clock per cohort
+    (launches, synchronizations and the out-of-range check per transaction)."""
+    import torch
+
+    from cachebridge_amd import synthetic
+    from cachebridge_amd.online.admission import MapperRequest, OnlineMapperAdmission
+    from cachebridge_amd.online.blocks import map_install_batch, map_install_block
+
+    out = {}
+    for size in (4, 16):
+        lengths = synthetic.request_lengths()[:size]
+        sh = synthetic.shape("batch", tokens=sum(lengths))
+        bh = synthetic.make_batch_handoff(sh, lengths)
+        ps = sh.page_size
+        cohort = [MapperRequest(f"req{i}", n) for i, n in enumerate(lengths)]
+        span = {r.request_id: sp for r, sp in zip(cohort, bh.spans)}
+        adm = OnlineMapperAdmission(max_cohort_requests=size)
+        budget = sum(lengths) + 32 * size
+
+        def transaction(r):
+            sp = span[r.request_id]
+            e = sp.target_offset // ps
+            map_install_block(bh.mapper, bh.source_pool,
+                              bh.source_slots[sp.source_offset:sp.source_offset + sp.num_tokens],
+                              bh.target_pool, start=0, stop=sp.num_tokens,
+                              block_table=bh.block_table[e:e + (sp.num_tokens + ps - 1) // ps], page_size=ps)
+            if bh.mapper.plan.read_errors():
+                raise RuntimeError("kernel flagged out-of-range rows")
+
+        def map_cohort(rs):
+            map_install_batch(bh.mapper, bh.source_pool, bh.source_slots, bh.target_pool,
+                              [span[r.request_id] for r in rs], block_table=bh.block_table, page_size=ps)
+            if bh.mapper.plan.read_errors():
+                raise RuntimeError("kernel flagged out-of-range rows")
+
+        def serial():
+            adm.execute_cohort(adm.plan(cohort, available_target_tokens=budget),
+                               mapper_transaction=transaction, query_batch=len)
+
+        def batched():
+            adm.execute_cohort_batched(adm.plan(cohort, available_target_tokens=budget),
+                                       map_cohort=map_cohort, publish=lambda r: None, query_batch=len)
+
+        times = {}
+        for name, fn in (("serial", serial), ("batched", batched)):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            times[name] = (time.perf_counter() - t0) / steps * 1e3
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        stream = torch.cuda.current_stream()
+        e0.record(stream)
+        for _ in range(steps):
+            bh.run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kernel_ms = e0.elapsed_time(e1) / steps
+        out[size] = dict(lengths=lengths, tokens=sum(lengths), serial_ms=times["serial"],
+                         batched_ms=times["batched"], kernel_ms=kernel_ms,
+                         bytes=synthetic.algorithmic_bytes(sh))
+        del bh
+        torch.cuda.empty_cache()
+    main4 = out[4]
+    gbs = main4["bytes"] / (main4["kernel_ms"] * 1e-3) / 1e9
+    return {
+        "metric": "admitted-cohort handoff, mapped+installed KV tokens/s (4 requests, one launch, FIFO publication)",
+        "value": round(main4["tokens"] / (main4["batched_ms"] * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(main4["batched_ms"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "the first 4 / 16 requests of " + WORKLOADS["batch"].split(" (")[0]
+                   + " lognormal lengths, TP4 share 40x2 -> 64x2 KV heads, head_dim 128, page 16"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "resolve_batch_kernel + map_install_stream_kernel<128, bf16, per-token positions>",
+                     "algorithmic_bytes_per_launch": main4["bytes"], "kernel_ms_mean": round(main4["kernel_ms"], 5)},
+        "cohorts": {str(k): {"lengths": v["lengths"], "tokens": v["tokens"],
+                             "serial_cohort_ms": round(v["serial_ms"], 4),
+                             "batched_cohort_ms": round(v["batched_ms"], 4),
+                             "batched_kernel_ms": round(v["kernel_ms"], 4),
+                             "serial_over_batched": round(v["serial_ms"] / v["batched_ms"], 2)}
+                    for k, v in out.items()},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -301,6 +392,8 @@ def main() -> int:
     ap.add_argument("--no-north-star", action="store_true")
     ap.add_argument("--delivery", action="store_true",
                     help="only time the selected-layer block delivery (receiver slots) at the TP4 share")
+    ap.add_argument("--cohort", action="store_true",
+                    help="only time an admitted cohort: per-request transactions vs one batched launch")
     ap.add_argument("--delta-state", action="store_true",
                     help="only time the recurrent-state transform (Qwen3.5-style hybrid model)")
     args = ap.parse_args()
@@ -312,6 +405,9 @@ def main() -> int:
         return 0
     if args.delivery:
         print(json.dumps(delivery_bench(args.steps, args.warmup)), flush=True)
+        return 0
+    if args.cohort:
+        print(json.dumps(cohort_bench(args.steps, args.warmup)), flush=True)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the handoff "
