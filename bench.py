@@ -219,6 +219,9 @@ def delta_state_bench(steps: int, warmup: int) -> dict:
     }
 
 
+SPIN_CYCLES = 200_000_000  # GPU spin ahead of short timed launches (tens of ms)
+
+
 def delivery_bench(steps: int, warmup: int) -> dict:
     """Receiver-side delivery of the TP4 share's selected source layers in
     2048-token blocks (two slots), timed per block; and the whole block-wise
@@ -245,25 +248,30 @@ def delivery_bench(steps: int, warmup: int) -> dict:
     for _ in range(warmup):
         pipelined()
     torch.cuda.synchronize()
-    # delivery kernel alone: one block per step, events on the delivery stream
-    times = []
+    # Delivery kernel alone: `steps` blocks back to back on the delivery stream.
+    # A block's gather (~20 us) is shorter than the host's deliver() call, so a
+    # spin kernel first keeps the GPU busy while the host enqueues them; the
+    # events then bracket GPU time only.
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(d.stream):
+        torch.cuda._sleep(SPIN_CYCLES)
+    e0.record(d.stream)
     for i in range(steps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(d.stream)
         d.deliver(i % 2, 0, block)
-        e1.record(d.stream)
         d.release(i % 2, d.stream)
-        times.append((e0, e1))
+    e1.record(d.stream)
     torch.cuda.synchronize()
-    deliver_ms = statistics.fmean(a.elapsed_time(b) for a, b in times)
+    deliver_ms = e0.elapsed_time(e1) / steps
     moved = 2 * 2 * len(d.layers) * block * sh.source_heads * sh.head_dim * 2  # read + write
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(SPIN_CYCLES)
     e0.record(compute)
     for _ in range(steps):
         pipelined()
     e1.record(compute)
     torch.cuda.synchronize()
     pipe_ms = e0.elapsed_time(e1) / steps
+    torch.cuda._sleep(SPIN_CYCLES)
     e0.record(compute)
     for _ in range(steps):
         h.run()

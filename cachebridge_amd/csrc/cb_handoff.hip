@@ -1186,6 +1186,13 @@ struct CopyArgs {
   int32_t* err;
 };
 
+// Each thread moves kCopyUnroll 16-byte pieces: first every piece's rows are
+// resolved (index loads), then every source piece is loaded, then stored, so
+// a thread keeps kCopyUnroll loads in flight instead of one dependent
+// index-load / load / store chain at a time. A workgroup covers 256 *
+// kCopyUnroll pieces (one pass), so many small workgroups fill the chip.
+constexpr int kCopyUnroll = 4;
+
 __global__ __launch_bounds__(256) void copy_rows_kernel(CopyArgs a) {
   const int lk = blockIdx.x / a.blocks_per_layer;  // layer * 2 + kind
   const int tb = blockIdx.x % a.blocks_per_layer;
@@ -1195,21 +1202,35 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(CopyArgs a) {
   const int t0 = tb * a.tokens_per_block;
   const int n = min(a.tokens_per_block, a.num_tokens - t0);
   const int cpr = a.chunks_per_row;
-  for (int idx = threadIdx.x; idx < n * cpr; idx += blockDim.x) {
-    const int t = t0 + idx / cpr;
-    const int ch = idx % cpr;
-    const int64_t sr = row_of(a.src, t);
-    const int64_t dr = row_of(a.dst, t);
-    if (sr < 0 || sr >= a.src.rows) {
-      if (a.err && ch == 0) atomicOr(a.err, 1);
-      continue;
+  const int total = n * cpr;
+  for (int base = threadIdx.x; base < total; base += blockDim.x * kCopyUnroll) {
+    int64_t so[kCopyUnroll], dof[kCopyUnroll];  // byte offsets; -1: piece not copied
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int idx = base + u * blockDim.x;
+      so[u] = -1;
+      dof[u] = -1;
+      if (idx < total) {
+        const int t = t0 + idx / cpr;
+        const int ch = idx % cpr;
+        const int64_t sr = row_of(a.src, t);
+        const int64_t dr = row_of(a.dst, t);
+        const bool sok = sr >= 0 && sr < a.src.rows;
+        const bool dok = dr >= 0 && dr < a.dst.rows;
+        if (a.err && ch == 0 && !(sok && dok)) atomicOr(a.err, sok ? 2 : 1);
+        if (sok && dok) {
+          so[u] = sr * a.src.row_stride_b + 16 * ch;
+          dof[u] = dr * a.dst.row_stride_b + 16 * ch;
+        }
+      }
     }
-    if (dr < 0 || dr >= a.dst.rows) {
-      if (a.err && ch == 0) atomicOr(a.err, 2);
-      continue;
-    }
-    const uint4 v = gload<uint4>(sbase + sr * a.src.row_stride_b + 16 * ch);
-    gstore<uint4>(dbase + dr * a.dst.row_stride_b + 16 * ch, v);
+    uint4 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u)
+      if (so[u] >= 0) v[u] = gload<uint4>(sbase + so[u]);
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u)
+      if (dof[u] >= 0) gstore<uint4>(dbase + dof[u], v[u]);
   }
 }
 
@@ -2218,7 +2239,7 @@ int cb_copy_rows(const cb_rows* src, const cb_rows* dst, int32_t num_layers, int
   if ((rc = to_dev_rows(*dst, eb, &a.dst))) return rc;
   a.num_tokens = num_tokens;
   a.chunks_per_row = row_elements * eb / 16;
-  a.tokens_per_block = std::max(1, 4096 / a.chunks_per_row);
+  a.tokens_per_block = std::max(1, 256 * kCopyUnroll / a.chunks_per_row);
   a.blocks_per_layer = (num_tokens + a.tokens_per_block - 1) / a.tokens_per_block;
   a.err = d_error_flag;
   const int64_t grid = static_cast<int64_t>(num_layers) * 2 * a.blocks_per_layer;
