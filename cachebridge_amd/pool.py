@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import torch
 
-from .plan import Rows, copy_rows, rows_from_layers, rows_from_page
+from .plan import Rows, copy_rows, rows_from_layers, rows_from_page, rows_from_stacked
 
 
 class PagedKVPool:
@@ -41,7 +41,6 @@ class PagedKVPool:
             self.v_data.zero_()
         self.k_buffer = list(self.k_data.unbind(0))
         self.v_buffer = list(self.v_data.unbind(0))
-        self._pointers: dict = {}
 
     def _get_key_buffer(self, layer: int) -> torch.Tensor:
         return self.k_buffer[layer - self.start_layer]
@@ -51,18 +50,19 @@ class PagedKVPool:
 
     def rows(self, *, index=None, block_table=None, page_size=None, index_offset: int = 0,
              head_offset: int = 0, tokens=None, layers: slice | None = None) -> Rows:
-        """Describe this pool (optionally a layer sub-range) with a token -> row index."""
-        ks, vs = self.k_buffer, self.v_buffer
+        """Describe this pool (optionally a layer sub-range) with a token -> row index.
+
+        K and V are each one ``[layers, rows, heads, head_dim]`` tensor, so the
+        description is a base address and a layer stride: no per-layer pointer
+        table and no per-layer checks on every call.
+        """
+        k, v = self.k_data, self.v_data
         if layers is not None:
-            ks, vs = ks[layers], vs[layers]
-            cache = None
-        else:
-            cache = self._pointers
+            k, v = k[layers], v[layers]
         if block_table is not None and page_size is None:
             page_size = self.page_size
-        return rows_from_layers(ks, vs, index=index, block_table=block_table, page_size=page_size,
-                                index_offset=index_offset, head_offset=head_offset,
-                                tokens=tokens, pointer_cache=cache)
+        return rows_from_stacked(k, v, index=index, block_table=block_table, page_size=page_size,
+                                 index_offset=index_offset, head_offset=head_offset, tokens=tokens)
 
     def set_kv_buffer(self, layer, loc, cache_k, cache_v, k_scale=None, v_scale=None,
                       layer_id_override=None):
