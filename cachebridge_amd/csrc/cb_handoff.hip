@@ -26,6 +26,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <numeric>
 #include <string>
 #include <type_traits>
@@ -1502,6 +1503,10 @@ struct cb_plan {
   int num_units = 0;
   int num_cus = 256;
   std::vector<int32_t> unit_weight;  // cost of one 16-token sub-tile of each unit
+  // Last cost-line split (it depends only on the blocks and the sub-tiles of
+  // each window class), reused by launches with the same shape.
+  mutable std::mutex split_mu;
+  mutable std::vector<int32_t> split_key, split_unit, split_sub;
   float* d_cos = nullptr;
   float* d_sin = nullptr;
   float* d_ucos = nullptr;
@@ -1915,7 +1920,19 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
       nb = std::min<int64_t>(nb, std::max<int64_t>(8, (unit_tokens + chunk - 1) / chunk));
     a.num_blocks = static_cast<int32_t>(std::max<int64_t>(8, nb / 8 * 8));
     grid_blocks = a.num_blocks;
-    split_cost_line(p, &a);
+    std::vector<int32_t> key{a.num_blocks, p->num_windows};
+    for (int c = 0; c < p->num_windows; ++c) key.push_back(a.cls_subtiles[c]);
+    const size_t nbk = static_cast<size_t>(a.num_blocks) + 1;
+    std::lock_guard<std::mutex> lock(p->split_mu);
+    if (key == p->split_key) {
+      std::copy(p->split_unit.begin(), p->split_unit.end(), a.blk_unit);
+      std::copy(p->split_sub.begin(), p->split_sub.end(), a.blk_sub);
+    } else {
+      split_cost_line(p, &a);
+      p->split_key = key;
+      p->split_unit.assign(a.blk_unit, a.blk_unit + nbk);
+      p->split_sub.assign(a.blk_sub, a.blk_sub + nbk);
+    }
   }
   const dim3 grid(static_cast<unsigned>(grid_blocks)), block(ws ? kStreamThreads : kThreads);
   if (ws) {
