@@ -51,6 +51,21 @@ def test_transform_matches_oracle(dtype, lead, k, v, kp, vp):
     _check(out, u, a, b)
 
 
+@pytest.mark.parametrize("shared_key_basis", [False, True])
+def test_many_entries_on_the_square_path(shared_key_basis):
+    # The 128 x 128 fp32 path at a Qwen3.5-like batch (more entries than
+    # resident workgroups, so several dispatch waves), with the key basis per
+    # entry and shared by every entry (batch stride 0).
+    g = torch.Generator().manual_seed(23)
+    u = torch.randn(1300, 128, 128, generator=g)
+    a = torch.randn(128, 128, generator=g) if shared_key_basis else torch.randn(1300, 128, 128, generator=g)
+    b = torch.randn(1300, 128, 128, generator=g)
+    out = arch.transform_delta_state(u.cuda(), a.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    assert out.shape == (1300, 128, 128)
+    _check(out, u, a, b)
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_shared_bases_broadcast_over_the_batch(dtype):
     g = torch.Generator().manual_seed(11)
