@@ -696,6 +696,30 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       trow[ct] = tr_a[ct];
       prow[ct] = pr_a[ct];
     }
+    // Keys with separate rotation tables: this sub-tile's rotation values are
+    // requested first, before this iteration's prefetches, so the epilogue's
+    // wait for them leaves those prefetches in flight (loads and stores share
+    // one in-order counter).
+    constexpr bool RSEP = IS_K && !SHARED;
+    float rcb[RSEP ? CT : 1][RSEP ? NGRP : 1][8], rsb[RSEP ? CT : 1][RSEP ? NGRP : 1][8];
+    if constexpr (RSEP) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const int64_t pos = PV ? prow[ct] : a.position_start + token_of(sub, ct);
+#pragma unroll
+        for (int hg = 0; hg < NGRP; ++hg)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int64_t off = tab_chunk<G>(pos, 2 * hg + u, g);
+            const float4 cv = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
+            const float4 sv = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
+            float* c = rcb[ct][hg] + 4 * u;
+            float* sn = rsb[ct][hg] + 4 * u;
+            c[0] = cv.x; c[1] = cv.y; c[2] = cv.z; c[3] = cv.w;
+            sn[0] = sv.x; sn[1] = sv.y; sn[2] = sv.z; sn[3] = sv.w;
+          }
+      }
+    }
 
     // Un-rotate (keys) and split the current sub-tile into B fragments.
     // Values stored as bf16 are their own single term: the loaded 16 bytes
@@ -837,14 +861,10 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
                 sbuf[e] = ts[ct][8 * hg + e];
               }
             } else {
-              const int64_t pos = PV ? prow[ct] : a.position_start + token_of(sub, ct);
 #pragma unroll
-              for (int u = 0; u < 2; ++u) {
-                const int64_t off = tab_chunk<G>(pos, 2 * hg + u, g);
-                const float4 cv = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
-                const float4 sv = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
-                cbuf[4 * u] = cv.x; cbuf[4 * u + 1] = cv.y; cbuf[4 * u + 2] = cv.z; cbuf[4 * u + 3] = cv.w;
-                sbuf[4 * u] = sv.x; sbuf[4 * u + 1] = sv.y; sbuf[4 * u + 2] = sv.z; sbuf[4 * u + 3] = sv.w;
+              for (int e = 0; e < 8; ++e) {
+                cbuf[e] = rcb[RSEP ? ct : 0][RSEP ? hg : 0][e];
+                sbuf[e] = rsb[RSEP ? ct : 0][RSEP ? hg : 0][e];
               }
             }
 #pragma unroll
