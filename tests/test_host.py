@@ -90,6 +90,25 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in out.stderr
 
 
+def test_bench_reads_committed_traffic_and_every_leg_has_a_summary():
+    import importlib.util
+    import re
+
+    spec = importlib.util.spec_from_file_location("bench_module", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    for workload in ("tp4", "full"):
+        traffic = bench.profiled_traffic("map_install_stream", workload)
+        text = (ROOT / "profiles" / f"map_install_stream_{workload}_traffic.md").read_text()
+        assert isinstance(traffic, int) and traffic > 0
+        assert f"traffic_bytes_per_launch = {traffic}" in text
+    assert bench.profiled_traffic("map_install_stream", "no_such_workload") is None
+    # every profile summary the design notes point to is committed
+    design = (ROOT / "DESIGN.md").read_text()
+    named = set(re.findall(r"profiles/([A-Za-z0-9_]+\.md)", design))
+    assert named and all((ROOT / "profiles" / n).exists() for n in named), sorted(named)
+
+
 def test_ragged_batch_lengths_and_bytes():
     lengths = synthetic.request_lengths()
     assert len(lengths) == 64 and sum(lengths) == 137_440
