@@ -589,8 +589,10 @@ __device__ void stream_run(const MapArgs& a, uint4* lds_w, float* lds_bias, int*
       const bool sok = s >= 0 && s < a.src.rows;
       const bool dok = d >= 0 && d < a.tgt.rows;
       errbits |= live ? (sok ? 0 : 1) | (dok ? 0 : 2) : 0;
+      // A token whose source row is out of range writes nothing: its store
+      // goes to the sink, so its target row keeps its old contents.
       sr[ct] = live && sok ? static_cast<int32_t>(s) : -1;
-      tr[ct] = live && dok ? static_cast<int32_t>(d) : -1;
+      tr[ct] = live && dok && sok ? static_cast<int32_t>(d) : -1;
     }
   };
 
@@ -988,6 +990,7 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
       tok[ct] = sub + wave * kGenWaveTokens + ct * 16 + col;
       valid[ct] = tok[ct] < wk.tok_hi;
     }
+    bool src_bad[kGenColTiles] = {};  // a support row out of range: the token writes nothing
     f32x4 acc[RT][kGenColTiles];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -1016,6 +1019,7 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
           if (row < 0 || row >= a.src.rows) {
             atomicOr(a.err, 1);
             ok = false;
+            src_bad[ct] = true;
           }
         }
         if (ok) {
@@ -1070,7 +1074,7 @@ __device__ void gen_run(const MapArgs& a, uint4* lds_w, const Work& wk, int4 met
 
 #pragma unroll
     for (int ct = 0; ct < kGenColTiles; ++ct) {
-      if (!valid[ct]) continue;
+      if (!valid[ct] || src_bad[ct]) continue;
       const int64_t row = row_of(a.tgt, tok[ct]);
       if (row < 0 || row >= a.tgt.rows) {
         atomicOr(a.err, 2);

@@ -34,17 +34,31 @@ class Rows:
     """One side of a launch: K/V layer buffers, row geometry and token -> row index.
 
     ``keep`` holds the tensors whose device memory the pointers refer to, so
-    they stay alive as long as the description.
+    they stay alive as long as the description. ``owned`` are the device
+    tensors this module allocated for the description (per-layer pointer
+    tables): every launch records them on its stream (``hold_for``), so the
+    caching allocator does not hand their memory out again while a kernel on
+    that stream may still read them, whichever stream allocated them and
+    however soon the description is dropped.
     """
 
     c: _lib.CbRows
     dtype: torch.dtype
     device: torch.device
     keep: list = field(default_factory=list)
+    owned: list = field(default_factory=list)
 
     @property
     def num_layers(self) -> int:
         return self.c.num_layers
+
+    def hold_for(self, stream: torch.cuda.Stream | None) -> None:
+        """Keep the owned tables allocated until ``stream``'s queued work is done."""
+        if not self.owned:
+            return
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        for t in self.owned:
+            t.record_stream(s)
 
 
 def _index_fields(index, block_table, page_size, index_offset, tokens):
@@ -112,7 +126,7 @@ def rows_from_layers(k_layers: Sequence[torch.Tensor], v_layers: Sequence[torch.
         host = torch.tensor(key, dtype=torch.int64)
         ptrs = host.to(first.device)
         # The table may be read by a kernel on another stream: let the upload
-        # land first (once per table; tables are cached by their pointers).
+        # land first (once per table when the caller keeps a cache).
         if first.device.type == "cuda":
             torch.cuda.current_stream(first.device).synchronize()
         if pointer_cache is not None:
@@ -133,7 +147,7 @@ def rows_from_layers(k_layers: Sequence[torch.Tensor], v_layers: Sequence[torch.
     c.index = idx_ptr
     c.index_offset = index_offset
     c.page_size = page_size or 0
-    return Rows(c, first.dtype, first.device, [ptrs, *keep, *k_layers, *v_layers])
+    return Rows(c, first.dtype, first.device, [ptrs, *keep, *k_layers, *v_layers], owned=[ptrs])
 
 
 def rows_from_stacked(k: torch.Tensor, v: torch.Tensor, *, index=None, block_table=None,
@@ -335,6 +349,8 @@ class HandoffPlan:
         req.tokens_per_workgroup = int(tokens_per_workgroup)
         _lib.check(self.lib.cb_map_install(self._handle, ctypes.byref(req),
                                            _lib.stream_handle(stream)))
+        source.hold_for(stream)
+        target.hold_for(stream)
 
     def workspace_bytes(self, spans: Sequence[RequestSpan]) -> int:
         """Device workspace bytes of a batched launch over ``spans``."""
@@ -372,6 +388,8 @@ class HandoffPlan:
         _lib.check(self.lib.cb_map_install_batch(self._handle, ctypes.byref(source.c),
                                                  ctypes.byref(target.c), arr, len(spans), ptr,
                                                  int(total.value), _lib.stream_handle(s)))
+        source.hold_for(s)
+        target.hold_for(s)
 
     def read_errors(self, stream: torch.cuda.Stream | None = None) -> int:
         """Synchronize ``stream`` and return/clear the device out-of-range flags."""
@@ -393,3 +411,5 @@ def copy_rows(src: Rows, dst: Rows, *, num_layers: int, num_tokens: int, row_ele
     _lib.check(lib.cb_copy_rows(ctypes.byref(src.c), ctypes.byref(dst.c), int(num_layers),
                                 int(num_tokens), int(row_elements), io_dtype_code(src.dtype),
                                 flag_ptr, _lib.stream_handle(stream)))
+    src.hold_for(stream)
+    dst.hold_for(stream)

@@ -13,6 +13,8 @@ HIP kernels.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from .plan import Rows, copy_rows, rows_from_layers, rows_from_page, rows_from_stacked
@@ -84,12 +86,32 @@ class PagedKVPool:
                   row_elements=self.head_num * self.head_dim)
 
 
+# Per-pool device tables of per-layer K/V pointers, for pools that are not a
+# PagedKVPool (one buffer per layer, e.g. SGLang's MHATokenToKVPool): built
+# once per pool and rebuilt only when the pool's buffers move.
+_POOL_TABLES: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+
+def _pool_cache(pool) -> dict | None:
+    try:
+        return _POOL_TABLES.setdefault(pool, {})
+    except TypeError:  # not weak-referenceable: build the table per call
+        return None
+
+
 def pool_rows(pool, *, index=None, block_table=None, page_size=None, index_offset: int = 0,
               head_offset: int = 0, tokens=None, pointer_cache: dict | None = None) -> Rows:
-    """Describe any ``MHATokenToKVPool``-like object for the HIP kernels."""
+    """Describe any ``MHATokenToKVPool``-like object for the HIP kernels.
+
+    A pool with one buffer per layer is described through a device table of
+    layer pointers. Without ``pointer_cache`` the table is kept per pool, so
+    it is uploaded once, not per call; launches record it on their stream.
+    """
     if isinstance(pool, PagedKVPool):
         return pool.rows(index=index, block_table=block_table, page_size=page_size,
                          index_offset=index_offset, head_offset=head_offset, tokens=tokens)
+    if pointer_cache is None:
+        pointer_cache = _pool_cache(pool)
     layers = range(pool.start_layer, pool.start_layer + pool.layer_num)
     ks = [pool._get_key_buffer(l) for l in layers]
     vs = [pool._get_value_buffer(l) for l in layers]

@@ -91,7 +91,8 @@ typedef struct cb_rows {
   const void* v_base;
   int64_t layer_stride; /* elements */
   int64_t row_stride;   /* elements */
-  int64_t rows;         /* rows per layer; rows outside [0, rows) are skipped and flagged */
+  int64_t rows;         /* rows per layer; a token whose source or target row is outside
+                           [0, rows) writes nothing and is flagged (cb_plan_read_errors) */
   int32_t num_layers;   /* layers addressable through this description */
   int32_t head_offset;
   int32_t heads;
