@@ -186,11 +186,14 @@ def install_unpublished(*, token_count, allocate, free, blocks, write, synchroni
                         publish, cancel_after_blocks=None):
     """Unpublished target transaction (``cb/online/blocks.py:114-171`` semantics).
 
-    ``blocks`` yields ``(start, stop, value)`` in order; ``write(value,
-    indices, start)`` enqueues the install; ``synchronize()`` fences it. No page
-    is published while any rank may still be writing: ``ready_vote`` runs on
-    every rank even after a local failure; a failed or cancelled transaction
-    frees its pages exactly once; a broken vote keeps them owned.
+    ``blocks`` yields ``(start, stop, value)`` in order; ``value`` is the
+    block's mapped page ``[2, layers, n, heads, D]`` (the reference's
+    ``map_write_block`` flow) or, for the fused install, the block's 1-D
+    source-row slice (``n`` entries). ``write(value, indices, start)`` enqueues
+    the install; ``synchronize()`` fences it. No page is published while any
+    rank may still be writing: ``ready_vote`` runs on every rank even after a
+    local failure; a failed or cancelled transaction frees its pages exactly
+    once; a broken vote keeps them owned.
     """
     indices = None
     error = None
@@ -201,7 +204,8 @@ def install_unpublished(*, token_count, allocate, free, blocks, write, synchroni
         if indices is None:
             raise RuntimeError("target pool allocation failed")
         for start, stop, value in blocks:
-            if start != cursor or not start < stop <= token_count or value.shape[2] != stop - start:
+            tokens = value.shape[2] if value.ndim >= 3 else value.shape[0]
+            if start != cursor or not start < stop <= token_count or tokens != stop - start:
                 raise ValueError("missing, duplicate or overlapping block")
             write(value, indices, start)
             synchronize()

@@ -186,8 +186,15 @@ class Handoff:
 
 
 def make_handoff(sh: Shape, device="cuda", *, target_pages: int | None = None,
-                 fill_target: str | None = None, source: torch.Tensor | None = None) -> Handoff:
-    """Build a resident handoff of shape ``sh`` on ``device``."""
+                 fill_target: str | None = None, source: torch.Tensor | None = None,
+                 device_source: bool = False) -> Handoff:
+    """Build a resident handoff of shape ``sh`` on ``device``.
+
+    Source values come from ``source_values`` (CPU generator), or with
+    ``device_source`` are drawn on the device from a seeded generator (same
+    distribution; fast for multi-GB pools, ``extras["source_values"]`` is then
+    None and the rows are read back from the pool where needed).
+    """
     spec = mapper_spec(sh)
     mapper = make_mapper(sh, spec, device=device)
     ps = sh.page_size
@@ -198,11 +205,23 @@ def make_handoff(sh: Shape, device="cuda", *, target_pages: int | None = None,
                            head_dim=sh.head_dim, page_size=ps, dtype=sh.dtype, device=device)
     src_page_list = fragmented_pages(src_total, src_pages_needed, 3000 + sh.seed)
     src_slots = slots_from_pages(src_page_list, n, ps)
-    values = source if source is not None else source_values(sh)
     src_slots_d = src_slots.to(device)
-    for l in range(sh.source_layers):
-        src_pool.k_buffer[l][src_slots_d] = values[0, l].to(device)
-        src_pool.v_buffer[l][src_slots_d] = values[1, l].to(device)
+    if device_source and source is None:
+        values = None
+        g = torch.Generator(device=device).manual_seed(5000 + sh.seed)
+        scale = torch.ones(sh.head_dim)
+        if sh.dtype == torch.bfloat16:
+            scale = torch.exp(torch.randn(sh.head_dim, generator=_gen(2000 + sh.seed)) * 0.5)
+        scale = scale.to(device)
+        for l in range(sh.source_layers):
+            for buf in (src_pool.k_buffer[l], src_pool.v_buffer[l]):
+                x = torch.randn((n, sh.source_heads, sh.head_dim), generator=g, device=device)
+                buf[src_slots_d] = (x * scale).to(sh.dtype)
+    else:
+        values = source if source is not None else source_values(sh)
+        for l in range(sh.source_layers):
+            src_pool.k_buffer[l][src_slots_d] = values[0, l].to(device)
+            src_pool.v_buffer[l][src_slots_d] = values[1, l].to(device)
     pages = target_pages or sh.target_pages or max(src_pages_needed * 2, 64)
     tgt_pool = PagedKVPool(layer_num=sh.target_layers, pages=pages, head_num=sh.target_heads,
                            head_dim=sh.head_dim, page_size=ps, dtype=sh.dtype, device=device,
