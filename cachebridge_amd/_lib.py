@@ -31,6 +31,8 @@ CB_INDEX_I64 = 2
 CB_INDEX_BLOCK_TABLE = 3
 CB_MAX_WINDOW_CLASSES = 4
 CB_MAX_SUPPORT = 16
+CB_NOALLOC_WORKSPACE_BYTES = 16777216
+CB_NOALLOC_MAX_TOKENS = 1398080
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -136,6 +138,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_c_void_p, ctypes.POINTER(CbRows), ctypes.POINTER(CbRows), ctypes.POINTER(CbSpan), _i32,
          _c_void_p, _i64, _c_void_p],
+    ),
+    "cb_map_install_batch_noalloc": (
+        ctypes.c_int,
+        [_c_void_p, ctypes.POINTER(CbRows), ctypes.POINTER(CbRows), ctypes.POINTER(CbSpan), _i32,
+         _c_void_p],
     ),
     "cb_copy_rows": (
         ctypes.c_int,

@@ -1500,6 +1500,14 @@ __global__ __launch_bounds__(256) void resolve_batch_kernel(BatchArgs b) {
 
 }  // namespace
 
+// Workspace of cb_map_install_batch_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends. Host code never uses this name
+// as an address (it is a host-side stand-in there); it uses the per-device
+// pointer that hipGetSymbolAddress returns (scratch_setup).
+static __device__ __align__(256) char scratch[CB_NOALLOC_WORKSPACE_BYTES];
+static_assert(3 * ((int64_t{CB_NOALLOC_MAX_TOKENS} * 4 + 255) / 256 * 256) <= CB_NOALLOC_WORKSPACE_BYTES,
+              "the no-allocation workspace holds CB_NOALLOC_MAX_TOKENS tokens");
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -2038,6 +2046,31 @@ int batch_layout(const cb_plan* p, const cb_span* spans, int32_t num_spans, Batc
 // token of the batch's token space, each section 256-byte aligned.
 int64_t batch_workspace(int64_t tokens) { return 3 * ((tokens * 4 + 255) / 256 * 256); }
 
+// Device address of `scratch` on each GPU, looked up once per device with
+// that device current (at plan creation on it).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_setup(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(CB_EINVAL, "device %d is beyond the %d devices the no-allocation workspace covers",
+                device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return CB_OK;
+  void* ptr = nullptr;
+  CB_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  if (!ptr) return fail(CB_EHIP, "hipGetSymbolAddress returned a null workspace address");
+  g_scratch_ptr[device] = ptr;
+  return CB_OK;
+}
+
+void* scratch_on(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_ptr[device];
+}
+
 }  // namespace
 
 extern "C" {
@@ -2132,7 +2165,9 @@ int cb_plan_create(const cb_plan_desc* d, cb_plan** out) {
   };
 
   cb_plan* p = new cb_plan();
-  const int rc = plan_build(d, order, same_group, p);
+  int rc = plan_build(d, order, same_group, p);
+  // The plan's device is current here: look up its no-allocation workspace.
+  if (rc == CB_OK) rc = scratch_setup(p->device);
   if (rc != CB_OK) {
     plan_free(p);
     return rc;
@@ -2258,6 +2293,26 @@ int cb_map_install_batch(const cb_plan* p, const cb_rows* source, const cb_rows*
   a.position_start = 0;
   return launch_map(p, a, L.cls_base, L.cls_count, 0,
                     default_chunk(p, static_cast<int>(std::min<int64_t>(L.total, INT32_MAX))), s);
+}
+
+int cb_map_install_batch_noalloc(const cb_plan* p, const cb_rows* source, const cb_rows* target,
+                                 const cb_span* spans, int32_t num_spans, void* stream) {
+  if (!p) return fail(CB_EINVAL, "null plan");
+  BatchLayout L;
+  int rc;
+  if ((rc = batch_layout(p, spans, num_spans, &L))) return rc;
+  const int64_t need = batch_workspace(L.total);
+  if (need > CB_NOALLOC_WORKSPACE_BYTES)
+    return fail(CB_EINVAL,
+                "batch of %lld kept tokens needs %lld workspace bytes; the no-allocation entry point "
+                "holds %lld (%lld tokens)",
+                static_cast<long long>(L.total), static_cast<long long>(need),
+                static_cast<long long>(CB_NOALLOC_WORKSPACE_BYTES),
+                static_cast<long long>(CB_NOALLOC_MAX_TOKENS));
+  void* ws = scratch_on(p->device);
+  if (!ws) return fail(CB_EINVAL, "no-allocation workspace is not set up on device %d", p->device);
+  return cb_map_install_batch(p, source, target, spans, num_spans, ws, CB_NOALLOC_WORKSPACE_BYTES,
+                              stream);
 }
 
 int cb_copy_rows(const cb_rows* src, const cb_rows* dst, int32_t num_layers, int32_t num_tokens,

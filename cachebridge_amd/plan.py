@@ -391,6 +391,28 @@ class HandoffPlan:
         source.hold_for(s)
         target.hold_for(s)
 
+    def launch_batch_noalloc(self, source: Rows, target: Rows, spans: Sequence[RequestSpan], *,
+                             stream: torch.cuda.Stream | None = None) -> None:
+        """``launch_batch`` without allocating: the workspace is the library's fixed per-GPU array.
+
+        Rejects batches beyond ``NOALLOC_MAX_TOKENS`` kept tokens. Calls that
+        overlap on one GPU share that array and race; calls on one stream are
+        ordered.
+        """
+        if self._handle is None:
+            raise RuntimeError("plan is closed")
+        if source.dtype != self.dtype or target.dtype != self.dtype:
+            raise ValueError(f"source/target dtype must be {self.dtype}")
+        if source.device != self.device or target.device != self.device:
+            raise ValueError("source, target and plan must be on the same device")
+        arr = _span_array(spans)
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        _lib.check(self.lib.cb_map_install_batch_noalloc(self._handle, ctypes.byref(source.c),
+                                                         ctypes.byref(target.c), arr, len(spans),
+                                                         _lib.stream_handle(s)))
+        source.hold_for(s)
+        target.hold_for(s)
+
     def read_errors(self, stream: torch.cuda.Stream | None = None) -> int:
         """Synchronize ``stream`` and return/clear the device out-of-range flags."""
         flags = ctypes.c_int32(0)

@@ -212,6 +212,27 @@ int cb_map_install_batch(const cb_plan* plan, const cb_rows* source, const cb_ro
                          const cb_span* spans, int32_t num_spans, void* d_workspace,
                          int64_t workspace_bytes, void* stream);
 
+/* Workspace limit of cb_map_install_batch_noalloc: 16 MiB per GPU, which
+   holds the resolved rows and positions (12 bytes per kept token, three
+   256-byte-aligned sections) of CB_NOALLOC_MAX_TOKENS tokens. */
+#define CB_NOALLOC_WORKSPACE_BYTES 16777216
+#define CB_NOALLOC_MAX_TOKENS 1398080
+
+/* cb_map_install_batch without a caller workspace and without any device
+   allocation: the resolve workspace is a fixed device array of
+   CB_NOALLOC_WORKSPACE_BYTES per GPU, looked up once per device at
+   cb_plan_create and held until the process ends. No counterpart in the
+   reference: this is for callers that cannot allocate device memory (code
+   under HIP graph capture, serving loops that forbid hipMalloc). Same rows,
+   row for row, as cb_map_install_batch. A batch needing more workspace is
+   rejected (CB_EINVAL) before anything is enqueued. Every call on one GPU
+   shares that GPU's array: calls that overlap on one GPU (two streams, or
+   a second call before the first completes on another stream) race; calls
+   on one stream are ordered. Asynchronous. */
+int cb_map_install_batch_noalloc(const cb_plan* plan, const cb_rows* source,
+                                 const cb_rows* target, const cb_span* spans,
+                                 int32_t num_spans, void* stream);
+
 /* Copy the first row_elements elements of rows of layers [0, num_layers)
    from src to dst, K and V: dst layer l row dst_row(t) <- src layer l row
    src_row(t) for t in [0, num_tokens). row_elements * element size must be a

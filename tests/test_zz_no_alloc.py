@@ -1,0 +1,89 @@
+"""GPU: the no-allocation batched install writes exactly what the allocating one writes.
+
+``cb_map_install_batch_noalloc`` is called through the C ABI on two ragged
+batches in a row, the second smaller than the first (so stale workspace
+contents from the first call would show), and each result is compared bit for
+bit with ``cb_map_install_batch`` given a torch-allocated workspace (that path
+is pinned against the oracle by the batch and full-size tests). A batch beyond
+the fixed workspace is rejected before anything is enqueued.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from cachebridge_amd import _lib, synthetic
+from cachebridge_amd.plan import RequestSpan, _span_array
+from cachebridge_amd.pool import PagedKVPool, pool_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _spans(lengths, positions, pages_total, seed):
+    g = torch.Generator().manual_seed(seed)
+    order = torch.randperm(pages_total, generator=g).to(torch.int32)
+    spans, src, entry = [], 0, 0
+    for n, p in zip(lengths, positions):
+        spans.append(RequestSpan(src, entry * 16, n, p, 0))
+        src += n
+        entry += (n + 15) // 16
+    assert entry <= pages_total
+    return spans, order[:entry].contiguous()
+
+
+def _zero_pool_like(pool):
+    return PagedKVPool(layer_num=pool.layer_num, pages=pool.pages, head_num=pool.head_num,
+                       head_dim=pool.head_dim, page_size=pool.page_size, dtype=pool.dtype,
+                       device=pool.device, fill="zeros")
+
+
+def test_noalloc_batch_equals_allocating_batch_on_two_calls():
+    lib = _lib.load()
+    batches = [([700, 1, 300, 1500, 17, 900, 64], [0, 5, 0, 40, 0, 100, 7]),
+               ([200, 33], [0, 3])]
+    tokens = sum(batches[0][0])
+    sh = synthetic.shape("tp4", tokens=tokens)
+    sh.target_layers = 6
+    pages = sum((n + 15) // 16 for n in batches[0][0]) * 2
+    h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros")
+    plan = h.mapper.plan
+    stream = torch.cuda.current_stream()
+    for call, (lengths, positions) in enumerate(batches):
+        print(f"no-alloc call {call}: {len(lengths)} requests, {sum(lengths)} tokens", flush=True)
+        spans, bt = _spans(lengths, positions, pages, seed=20 + call)
+        bt = bt.to(h.target_pool.device)
+        want, got = _zero_pool_like(h.target_pool), _zero_pool_like(h.target_pool)
+        src = pool_rows(h.source_pool, index=h.source_slots)
+        plan.launch_batch(src, pool_rows(want, block_table=bt, page_size=16), spans)
+        tgt = pool_rows(got, block_table=bt, page_size=16)
+        arr = _span_array(spans)
+        _lib.check(lib.cb_map_install_batch_noalloc(plan._handle, ctypes.byref(src.c),
+                                                    ctypes.byref(tgt.c), arr, len(spans),
+                                                    _lib.stream_handle(stream)))
+        torch.cuda.synchronize()
+        assert plan.read_errors() == 0
+        assert torch.equal(got.k_data, want.k_data)
+        assert torch.equal(got.v_data, want.v_data)
+        assert int(got.v_data.abs().sum()) > 0
+
+
+def test_noalloc_batch_beyond_the_workspace_is_rejected_before_launch():
+    lib = _lib.load()
+    sh = synthetic.shape("tp4", tokens=64)
+    sh.target_layers = 2
+    h = synthetic.make_handoff(sh, target_pages=16, fill_target="zeros")
+    per = 40000
+    count = _lib.CB_NOALLOC_MAX_TOKENS // per + 1
+    spans = [RequestSpan(0, 0, per, 0, 0)] * count
+    src = pool_rows(h.source_pool, index=h.source_slots)
+    tgt = pool_rows(h.target_pool, block_table=h.block_table, page_size=16)
+    arr = _span_array(spans)
+    with pytest.raises(ValueError, match="no-allocation"):
+        _lib.check(lib.cb_map_install_batch_noalloc(h.mapper.plan._handle, ctypes.byref(src.c),
+                                                    ctypes.byref(tgt.c), arr, len(spans),
+                                                    _lib.stream_handle(None)))
+    torch.cuda.synchronize()
+    assert int(h.target_pool.k_data.abs().sum()) == 0
