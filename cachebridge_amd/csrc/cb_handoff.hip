@@ -934,6 +934,334 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
 }
 
 // ---------------------------------------------------------------------------
+// Support kernel (support s > 1, head_dim 128, bf16 K/V): a blocked GEMM.
+//
+// A target job's feature row is the concatenation of its s source rows, so
+// each job is a [T x s*128] . [s*128 x 128] contraction (the shipped top-8
+// recipe: 1024 input dims). A workgroup of 4 waves computes one 128-token
+// block of one job; two workgroups run on every CU. The input dims are
+// streamed in 2*s stages of 64 dims -- k-step pair {q, q + 2} (32 first-half
+// dims and their RoPE partners) of support member k, all members for q = 0
+// first -- through one LDS stage buffer:
+//   - W of the stage (8 row tiles x 2 k-steps x 2 terms, 32 KB) is loaded one
+//     stage ahead into registers;
+//   - the stage's input (128 tokens x 64 dims) is loaded two stages ahead and
+//     produced by the 256 threads, one token and 8 dims (+ partners) per
+//     task, two tasks each: keys are un-rotated and split into bf16 terms
+//     (the thread's un-rotation values of the current q stay in registers
+//     for s stages), values are written as loaded;
+//   - wave (h, c) multiplies row tiles {h*2 + q', +4} (an output half with
+//     its RoPE partners) by column tiles 4c .. 4c + 3 (64 tokens),
+//     accumulating across all stages in 64 VGPRs: each W fragment read from
+//     LDS feeds 4 column tiles and each input fragment 4 row tiles.
+// A stage is: multiply; barrier; write the next stage's W and input;
+// barrier. While one workgroup waits at a barrier or writes, the other keeps
+// the CU's MFMAs busy. Blocks are ordered job-major within each window class
+// and cut into one contiguous eighth per XCD, so an XCD's CUs run the blocks
+// of one job together and read its W (512 KB at s = 8) from their shared L2.
+// W is packed with the group output permutation (grp_out_dim); the epilogue
+// (bias as the first accumulator input, target RoPE, cast) stores whole
+// 64-byte chunks of the target rows.
+// ---------------------------------------------------------------------------
+
+constexpr int kSupTile = 128;                 // tokens per workgroup block
+constexpr int kSupWaves = 4;
+constexpr int kSupThreads = kSupWaves * kWave;
+
+// Output dim of row r (0..15) of row tile rt (0..7): tile rt = p*4 + h*2 + q
+// holds in lane group g = r / 4 the dims p*64 + h*32 + g*8 + q*4 + r % 4, so
+// the wave that owns half h (tiles h*2 + q and their RoPE partners, +4) has 8
+// consecutive dims in each lane group and each store instruction writes
+// whole 64-byte chunks of a target row.
+__host__ __device__ inline int grp_out_dim(int rt, int r) {
+  return (rt >> 2) * 64 + ((rt >> 1) & 1) * 32 + (r >> 2) * 8 + (rt & 1) * 4 + (r & 3);
+}
+
+// The stage buffer: W [row tile][k-step][term][lane] (32 KB) and the input
+// [column tile][k-step][term][lane] (32 KB).
+struct SupStage {
+  uint4 w[8][2][2][kWave];
+  uint4 x[8][2][2][kWave];
+};
+
+template <bool IS_K, bool SHARED, bool POS>
+__device__ void support_run(const MapArgs& a, SupStage& B, int32_t* trow, int32_t* tpos, float* bias,
+                            int job, int tok_lo, int tok_hi) {
+  // No implicit contraction: every fused multiply-add is written out.
+#pragma clang fp contract(off)
+  constexpr int D = 128, HALF = 64;
+  constexpr int kind = IS_K ? CB_KIND_K : CB_KIND_V;
+  constexpr int XT = IS_K ? 2 : 1;  // input terms (values are bf16-exact)
+  const int S = a.support;
+  const int nstage = 2 * S;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g = lane >> 4, col = lane & 15;
+  // Consumer: output half hh, column tiles 4cb .. 4cb + 3.
+  const int hh = wave >> 1, cb = wave & 1;
+
+  const int* jm = reinterpret_cast<const int*>(a.jobs + job);
+  const int mx = cload(jm), meta_y = cload(jm + 1);
+  const int sth = (meta_y >> 16) & 0xff, tth = (meta_y >> 24) & 0xff;
+  gptr tbase = const_cast<gptr>(layer_base(a.tgt, kind, mx & 0xffff)) +
+               static_cast<int64_t>((mx >> 16) - a.tgt.head_offset) * D * 2 + (hh * 32 + g * 8) * 2;
+  gptr sink = as_global(a.sink) + lane * 512;
+  gcptr zrow = as_global(a.zero);
+  const int32_t* pj = a.pairs + static_cast<size_t>(job) * S;
+  const CB_GLOBAL float* ucos = gtab(SHARED ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* usin = gtab(SHARED ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
+  const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
+  gcptr wjob = as_global(a.w + static_cast<size_t>(job) * S * Gm<128, uint16_t>::W_U4) + lane * 16;
+
+  // Producer tasks j = 0, 1: column tile 2 * wave + j, token 16 * (2 * wave
+  // + j) + col, first-half dims 16g + 8q .. +7 and their partners. One row
+  // index serves every support member (they are layers of one source pool).
+  const int n = tok_hi - tok_lo;
+  int64_t soff[2];
+  int pos[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int pt = 16 * (2 * wave + j) + col;
+    const int tk = tok_lo + min(pt, n - 1);
+    const bool live = pt < n;
+    const int64_t srow = row_of(a.src, tk);
+    const int64_t drow = row_of(a.tgt, tk);
+    const bool sok = srow >= 0 && srow < a.src.rows;
+    const bool dok = drow >= 0 && drow < a.tgt.rows;
+    if (live && !(sok && dok) && g == 0) atomicOr(a.err, (sok ? 0 : 1) | (dok ? 0 : 2));
+    soff[j] = live && sok ? srow * a.src.row_stride_b : -1;
+    pos[j] = position_of(a, tk);
+    if (g == 0) {
+      // A token whose source row is out of range writes nothing (sink).
+      trow[pt] = live && sok && dok ? static_cast<int32_t>(drow) : -1;
+      tpos[pt] = pos[j];
+    }
+  }
+  if (threadIdx.x < D) bias[threadIdx.x] = a.bias[static_cast<size_t>(job) * D + threadIdx.x];
+
+  // Stage t: q = t / S, support member k = t % S, k-steps {q, q + 2}.
+  auto load_w = [&](int t, uint4 (&wv)[8]) {
+    const int q = t / S, k = t - q * S;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int f = j * kSupWaves + wave;  // (row tile, k-step slot, term)
+      const int rt = f >> 2, kk = (f >> 1) & 1, tm = f & 1;
+      const int ks = q + 2 * kk;
+      wv[j] = gload<uint4>(wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
+    }
+  };
+  auto store_w = [&](const uint4 (&wv)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int f = j * kSupWaves + wave;
+      B.w[f >> 2][(f >> 1) & 1][f & 1][lane] = wv[j];
+    }
+  };
+  auto load_x = [&](int t, uint4 (&xv)[2][2]) {
+    const int tc = min(t, nstage - 1);  // past the end: clamped, unused
+    const int q = tc / S, k = tc - q * S;
+    const int pr = cload(pj + k);
+    gcptr base = layer_base(a.src, kind, pr & 0xffff) + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * D * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      gcptr p = (soff[j] >= 0 ? base + soff[j] : zrow) + (16 * g + 8 * q) * 2;
+      xv[j][0] = gload<uint4>(p);
+      xv[j][1] = gload<uint4>(p + HALF * 2);
+    }
+  };
+  // Un-rotation values of both tasks for k-step pair q: frequencies 16g + 8q + [0, 8).
+  float uc[2][8], us[2][8];
+  auto load_tab = [&](int q) {
+    if constexpr (IS_K) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t off = tab_chunk<16>(pos[j], 2 * q + u, g);
+          const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(ucos + off);
+          const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(usin + off);
+          uc[j][4 * u] = c4.x; uc[j][4 * u + 1] = c4.y; uc[j][4 * u + 2] = c4.z; uc[j][4 * u + 3] = c4.w;
+          us[j][4 * u] = s4.x; us[j][4 * u + 1] = s4.y; us[j][4 * u + 2] = s4.z; us[j][4 * u + 3] = s4.w;
+        }
+    }
+  };
+  auto produce_x = [&](const uint4 (&xv)[2][2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ct = 2 * wave + j;
+      if constexpr (IS_K) {
+        float x1[8], x2[8];
+        unpack16<uint16_t>(xv[j][0], x1);
+        unpack16<uint16_t>(xv[j][1], x2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float k1 = __builtin_fmaf(x1[e], uc[j][e], x2[e] * us[j][e]);
+          const float k2 = __builtin_fmaf(x2[e], uc[j][e], -(x1[e] * us[j][e]));
+          x1[e] = k1;
+          x2[e] = k2;
+        }
+        uint32_t t1[2][4], t2[2][4];
+        split_terms<2, 8>(x1, t1);
+        split_terms<2, 8>(x2, t2);
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          B.x[ct][0][x][lane] = make_uint4(t1[x][0], t1[x][1], t1[x][2], t1[x][3]);
+          B.x[ct][1][x][lane] = make_uint4(t2[x][0], t2[x][1], t2[x][2], t2[x][3]);
+        }
+      } else {
+        B.x[ct][0][0][lane] = xv[j][0];
+        B.x[ct][1][0][lane] = xv[j][1];
+      }
+    }
+  };
+
+  f32x4 acc[4][4];  // [row tile p*2 + q'][column tile]
+  auto multiply = [&](bool first) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 xv[4][XT];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int x = 0; x < XT; ++x) xv[c][x] = __builtin_bit_cast(bf16x8, B.x[4 * cb + c][kk][x][lane]);
+      bf16x8 wv[4][2];
+#pragma unroll
+      for (int rl = 0; rl < 4; ++rl) {
+        const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, B.w[rt][kk][tm][lane]);
+      }
+      int pi = 0;
+      for_products<XT, 2>([&](int ii, int jj) {
+#pragma unroll
+        for (int rl = 0; rl < 4; ++rl)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            f32x4 cin;
+            if (first && kk == 0 && pi == 0) {
+              const float* bp = bias + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
+              cin = f32x4{bp[0], bp[1], bp[2], bp[3]};
+            } else {
+              cin = acc[rl][c];
+            }
+            acc[rl][c] = mfma(wv[rl][jj], xv[c][ii], cin);
+          }
+        ++pi;
+      });
+    }
+  };
+
+  // Prologue: stage 0 written; stage 1's W and input requested.
+  uint4 wn[8], xa[2][2], xb[2][2];
+  load_w(0, wn);
+  load_x(0, xa);
+  load_x(1, xb);
+  load_tab(0);
+  __syncthreads();  // trow, tpos and bias written (and a previous block's LDS reads done)
+  store_w(wn);
+  produce_x(xa);
+  // Barriers inside the stage loop fence LDS only, so the loads issued for
+  // later stages stay in flight (a full barrier would wait for them).
+  auto lds_barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  load_w(1, wn);
+  load_x(2, xa);
+  lds_barrier();
+  // Stage t multiplies; then the buffer is rewritten with stage t+1 (W from
+  // wn, input from the set loaded two stages earlier) while stage t+2's W
+  // and stage t+3's input are requested. xb / xa alternate as the input of
+  // the next stage.
+  auto stage = [&](int t, uint4 (&x_next)[2][2]) {
+    multiply(t == 0);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();  // every wave has read stage t
+    if (t + 1 < nstage) {
+      if (t + 1 == S) load_tab(1);  // the second k-step pair starts
+      store_w(wn);
+      produce_x(x_next);
+      if (t + 2 < nstage) load_w(t + 2, wn);
+      load_x(t + 3, x_next);  // this set was just consumed; it becomes stage t+3's input
+      lds_barrier();
+    }
+  };
+  for (int t = 0; t < nstage; t += 2) {
+    stage(t, xb);
+    stage(t + 1, xa);
+  }
+
+  // Epilogue: target RoPE, cast, store.
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int tok = (4 * cb + c) * 16 + col;
+    const int row = trow[tok];
+    float y1[8], y2[8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y1[4 * q + i] = acc[q][c][i];
+        y2[4 * q + i] = acc[2 + q][c][i];
+      }
+    if constexpr (IS_K) {
+      const int tp = tpos[tok];
+      float cv[8], sv[8];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int64_t off = tab_chunk<16>(tp, 2 * (g & 1) + u, 2 * hh + (g >> 1));
+        const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
+        const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
+        cv[4 * u] = c4.x; cv[4 * u + 1] = c4.y; cv[4 * u + 2] = c4.z; cv[4 * u + 3] = c4.w;
+        sv[4 * u] = s4.x; sv[4 * u + 1] = s4.y; sv[4 * u + 2] = s4.z; sv[4 * u + 3] = s4.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a1 = y1[e], a2 = y2[e];
+        y1[e] = __builtin_fmaf(a1, cv[e], -(a2 * sv[e]));
+        y2[e] = __builtin_fmaf(a2, cv[e], a1 * sv[e]);
+      }
+    }
+    uint32_t o1[4], o2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o1[i] = pack_bf16(y1[2 * i], y1[2 * i + 1]);
+      o2[i] = pack_bf16(y2[2 * i], y2[2 * i + 1]);
+    }
+    gptr dst = row >= 0 ? tbase + static_cast<int64_t>(row) * a.tgt.row_stride_b : sink;
+    gstore<uint4>(dst, make_uint4(o1[0], o1[1], o1[2], o1[3]));
+    gstore<uint4>(dst + HALF * 2, make_uint4(o2[0], o2[1], o2[2], o2[3]));
+  }
+}
+
+template <bool POS>
+__global__ __launch_bounds__(kSupThreads, 2) void map_install_support_kernel(MapArgs a) {
+  __shared__ SupStage B;
+  __shared__ int32_t trow[kSupTile];
+  __shared__ int32_t tpos[kSupTile];
+  __shared__ float bias[128];
+  // Item L of XCD b & 7's contiguous eighth: window class, then job, then
+  // 128-token block, so an XCD's CUs run the blocks of one job together.
+  const int per = a.padded_items >> 3;
+  const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (L >= a.total_items) return;
+  int c = 0;
+  while (c + 1 < a.ncls && L >= a.cls_item_begin[c + 1]) ++c;
+  const int lc = L - a.cls_item_begin[c];
+  const int nch = a.cls_nchunks[c];
+  const int job = __builtin_amdgcn_readfirstlane(cload(a.unit_job + a.cls_unit_begin[c] + lc / nch));
+  const int lo = a.cls_tok_first[c] + (lc % nch) * kSupTile;
+  const int hi = min(lo + kSupTile, a.cls_tok_first[c] + a.cls_tok_count[c]);
+  const int* mp = reinterpret_cast<const int*>(a.jobs + job);
+  const int meta_y = cload(mp + 1), meta_z = cload(mp + 2);
+  if ((meta_y & 0xff) == CB_KIND_K) {
+    if (meta_z & kJobSharedTables) support_run<true, true, POS>(a, B, trow, tpos, bias, job, lo, hi);
+    else support_run<true, false, POS>(a, B, trow, tpos, bias, job, lo, hi);
+  } else {
+    support_run<false, false, POS>(a, B, trow, tpos, bias, job, lo, hi);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // General kernel (any support s): W block of the current support staged in
 // LDS, source fragments in registers; each wave covers all output dims of 32
 // tokens. Output dims permuted so lane group g holds dims [g*D/8, (g+1)*D/8)
@@ -1128,7 +1456,7 @@ __global__ __launch_bounds__(kThreads) void map_install_gen_kernel(MapArgs a) {
 
 // Pack fp32 W[orig][s*D][D] into bf16 split terms in MFMA A-fragment order,
 // and permute the bias to sorted job order.
-template <int D, int NTW>
+template <int D, int NTW, bool GROUP>
 __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __restrict__ bias,
                                     const int32_t* __restrict__ order, int njobs, int S,
                                     uint16_t* __restrict__ wp, float* __restrict__ bp) {
@@ -1143,7 +1471,7 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
     const int t = rem % NTW; rem /= NTW;
     const int ks = rem % KS; rem /= KS;
     const int rt = rem % RT; rem /= RT;
-    const int fo = gen_out_dim(D, rt, lane & 15);
+    const int fo = GROUP ? grp_out_dim(rt, lane & 15) : gen_out_dim(D, rt, lane & 15);
     const int k = rem % S; rem /= S;
     const int j = static_cast<int>(rem);
     const int src_job = order[j];
@@ -1517,6 +1845,7 @@ struct cb_plan {
   cb_plan_info info{};
   int ntw = 2;
   int elem_bytes = 2;
+  bool support_gemm = false;  // support > 1, head_dim 128, bf16: map_install_support_kernel
   int num_windows = 1;
   int window_size[kMaxClasses] = {0, 0, 0, 0};
   int cls_unit_begin[kMaxClasses] = {0, 0, 0, 0};
@@ -1601,10 +1930,10 @@ int to_dev_rows(const cb_rows& r, int elem_bytes, DevRows* out) {
   return CB_OK;
 }
 
-template <int D, int NTW>
+template <int D, int NTW, bool GROUP = false>
 void launch_pack(const cb_plan_desc* d, const int32_t* d_order, uint16_t* wp, float* bp) {
-  hipLaunchKernelGGL((pack_weights_kernel<D, NTW>), dim3(1024), dim3(256), 0, 0, d->d_weight, d->d_bias,
-                     d_order, d->num_jobs, d->support, wp, bp);
+  hipLaunchKernelGGL((pack_weights_kernel<D, NTW, GROUP>), dim3(1024), dim3(256), 0, 0, d->d_weight,
+                     d->d_bias, d_order, d->num_jobs, d->support, wp, bp);
 }
 
 template <typename SameGroup>
@@ -1615,6 +1944,7 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   CB_HIP(hipGetDevice(&p->device));
   p->ntw = d->io_dtype == CB_DTYPE_BF16 ? 2 : 3;
   p->elem_bytes = d->io_dtype == CB_DTYPE_BF16 ? 2 : 4;
+  p->support_gemm = S > 1 && D == 128 && p->ntw == 2;
   p->num_windows = d->num_windows;
   for (int c = 0; c < kMaxClasses; ++c) {
     p->window_size[c] = c < d->num_windows ? d->window_size[c] : 0;
@@ -1742,6 +2072,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
       launch_pack<64, 2>(d, d_order, wp, p->d_bias);
     else if (D == 64)
       launch_pack<64, 3>(d, d_order, wp, p->d_bias);
+    else if (p->support_gemm)
+      launch_pack<128, 2, true>(d, d_order, wp, p->d_bias);
     else
       launch_pack<128, 2>(d, d_order, wp, p->d_bias);
     e = hipGetLastError();
@@ -1979,6 +2311,10 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
       if (pv) hipLaunchKernelGGL((map_install_stream_kernel<64, float, true>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((map_install_stream_kernel<64, float, false>), grid, block, 0, s, a);
     }
+  } else if (p->support_gemm) {
+    static_assert(kGenSubTokens == kSupTile, "one 128-token block per item");
+    if (a.pos) hipLaunchKernelGGL((map_install_support_kernel<true>), grid, dim3(kSupThreads), 0, s, a);
+    else hipLaunchKernelGGL((map_install_support_kernel<false>), grid, dim3(kSupThreads), 0, s, a);
   } else {
     if (D == 128 && p->ntw == 2)
       hipLaunchKernelGGL((map_install_gen_kernel<128, uint16_t>), grid, block, 0, s, a);

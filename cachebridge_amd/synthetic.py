@@ -20,6 +20,11 @@ Shapes (source model -> target model, per GPU):
                260 GB next to the source pool, more than one GPU holds).
 - ``batch_full``: the same requests at the whole-model 64x8 geometry, with the
                target pool at 50% occupancy (2x the batch's pages).
+- ``tp4_s8`` / ``full_s8``: the shipped support-8 recipe's structure at the
+               TP4 share and the whole model: every target layer reads 8
+               distinct source layers (its depth-matched layer first, then 7
+               seeded neighbours within 12 layers), shared by K and V and by
+               every head, with head identity; maps are [8*128, 128].
 
 Source keys are treated as stored RoPE-rotated (as SGLang stores them); the
 map is A ~ N(0, 1/(s*D)), b ~ N(0, 0.01); bf16 sources are N(0,1) times a
@@ -55,6 +60,7 @@ class Shape:
     target_pages: int | None = None
     page_size: int = 16
     seed: int = 0
+    support: int = 1                     # source (layer, head) pairs per target (support-s maps)
 
 
 def shape(name: str, tokens: int | None = None) -> Shape:
@@ -74,6 +80,11 @@ def shape(name: str, tokens: int | None = None) -> Shape:
                   target_theta=[1e6 if g else 1e4 for g in glob],
                   windows=[None if g else 1024 for g in glob], head_map="half",
                   target_pages=1024, seed=5)
+    elif name in ("tp4_s8", "full_s8"):
+        heads = 2 if name == "tp4_s8" else 8
+        s = Shape(name, 40, heads, 64, heads, 128, 4096, torch.bfloat16, [], head_map="identity",
+                  target_pages=65536 if name == "tp4_s8" else 8192, seed=8 if name == "tp4_s8" else 9,
+                  support=8)
     elif name in ("batch", "batch_full"):
         heads = 2 if name == "batch" else 8
         s = Shape(name, 40, heads, 64, heads, 128, sum(request_lengths()), torch.bfloat16, sel16,
@@ -101,6 +112,8 @@ def mapper_spec(sh: Shape) -> dict:
     """Assignment and fp32 maps of a shape (CPU tensors)."""
     g = _gen(1000 + sh.seed)
     lt, ht, d = sh.target_layers, sh.target_heads, sh.head_dim
+    if sh.support > 1:
+        return _support_spec(sh, g)
     if sh.selected:
         selected = list(sh.selected)
     else:
@@ -120,6 +133,34 @@ def mapper_spec(sh: Shape) -> dict:
         "k_bias": torch.randn(lt, ht, d, generator=g) * 0.1,
         "v_bias": torch.randn(lt, ht, d, generator=g) * 0.1,
         "selected": selected,
+    }
+
+
+def support_layers(sh: Shape, g: torch.Generator) -> list[list[int]]:
+    """Per target layer, ``sh.support`` distinct source layers: the depth-matched
+    layer first, then seeded neighbours within 12 layers (the recipe's shape)."""
+    out = []
+    ls, lt = sh.source_layers, sh.target_layers
+    for l in range(lt):
+        c = round(l * (ls - 1) / max(lt - 1, 1))
+        near = [x for x in range(max(0, c - 12), min(ls, c + 13)) if x != c]
+        pick = torch.randperm(len(near), generator=g)[: sh.support - 1].tolist()
+        out.append([c] + [near[i] for i in pick])
+    return out
+
+
+def _support_spec(sh: Shape, g: torch.Generator) -> dict:
+    lt, ht, d, s = sh.target_layers, sh.target_heads, sh.head_dim, sh.support
+    layers = torch.tensor(support_layers(sh, g), dtype=torch.int64)      # [lt, s]
+    std = 1.0 / math.sqrt(s * d)
+    return {
+        "assign_layer": layers[:, None, :].expand(lt, ht, s).clone(),
+        "assign_head": torch.arange(ht).view(1, ht, 1).expand(lt, ht, s).clone(),
+        "k_weight": torch.randn(lt, ht, s * d, d, generator=g) * std,
+        "v_weight": torch.randn(lt, ht, s * d, d, generator=g) * std,
+        "k_bias": torch.randn(lt, ht, d, generator=g) * 0.1,
+        "v_bias": torch.randn(lt, ht, d, generator=g) * 0.1,
+        "selected": sorted({int(x) for x in layers.flatten()}),
     }
 
 
@@ -243,7 +284,7 @@ def algorithmic_bytes(sh: Shape, tokens_per_layer: list | None = None) -> int:
         tokens_per_layer = [window_tokens(sh, l) for l in range(sh.target_layers)]
     write = 2 * e * d * sum(t * sh.target_heads for t in tokens_per_layer)
     read = 2 * e * d * len(pairs) * sh.tokens
-    weights = 4 * 2 * sh.target_layers * sh.target_heads * (d * d + d)
+    weights = 4 * 2 * sh.target_layers * sh.target_heads * (sh.support * d * d + d)
     return write + read + weights + 8 * sh.tokens
 
 
@@ -254,7 +295,7 @@ def window_tokens(sh: Shape, layer: int) -> int:
 
 def algorithmic_flops(sh: Shape) -> int:
     d = sh.head_dim
-    return sum(2 * 2 * window_tokens(sh, l) * sh.target_heads * d * d
+    return sum(2 * 2 * window_tokens(sh, l) * sh.target_heads * sh.support * d * d
                for l in range(sh.target_layers))
 
 

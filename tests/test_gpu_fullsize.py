@@ -7,7 +7,9 @@ Workloads (``cachebridge_amd.synthetic``):
 - Gemma-style target: 62x16 with 52 sliding-window layers (window 1024) and
   10 global layers, 8192 tokens;
 - 64 ragged requests (137,440 tokens) at the TP4 share into one pool at 85%
-  occupancy.
+  occupancy;
+- the shipped support-8 recipe's structure (every target layer reads 8 source
+  layers, maps [1024, 128]) at the TP4 share and the whole model, 4096 tokens.
 
 Each launch is checked for: error word 0; every pool row outside the
 request's slots (and, per windowed layer, outside its window) bit-unchanged;
@@ -49,7 +51,8 @@ def _release_memory():
 
 
 @pytest.mark.parametrize("name,layers", [("tp4", SAMPLE_64), ("full32k", SAMPLE_64),
-                                         ("gemma", SAMPLE_GEMMA)])
+                                         ("gemma", SAMPLE_GEMMA), ("tp4_s8", SAMPLE_64),
+                                         ("full_s8", SAMPLE_64)])
 def test_full_size_handoff(name, layers):
     sh = synthetic.shape(name)
     t_count = sh.tokens
