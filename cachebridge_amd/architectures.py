@@ -1,34 +1,72 @@
 """Structured-state installs on either side of the handoff (Gemma 3, Qwen3.5).
 
-Host-side mirrors of the reference's per-architecture install contracts and
-the GPU recurrent-state transform:
+The install contracts are the reference's (same functions, arguments, errors
+and messages): ``materialize_kv`` / ``install_kv`` for the Gemma 3
+local/global cache roster (``cb/architectures/gemma3.py:38-94``);
+``required_replay``, ``install_attention_kv`` and ``install_linear_state``
+for Qwen3.5 (``cb/architectures/qwen35.py:64-160``). Every install is
+all-or-nothing: nothing in the cache changes unless every check passed.
 
-- ``materialize_kv`` / ``install_kv``: Gemma 3 local/global cache roster,
-  ``cb/architectures/gemma3.py:38-94``. Every layer is validated before any
-  layer is mutated; sliding layers record the whole prefix length.
-- ``transform_delta_state``: Qwen3.5 DeltaNet memory mapped as ``A^T U B``,
-  ``cb/architectures/qwen35.py:52-61``, computed by the HIP kernel behind
-  ``cb_delta_state_transform`` (16x16x4 fp32 / fp64 MFMAs). Inputs must be GPU
-  tensors; there is no CPU path.
-- ``required_replay``, ``install_attention_kv``, ``install_linear_state``:
-  ``cb/architectures/qwen35.py:64-160``.
+How it is done here: a target cache layer is first given a role
+(``_role``: full or sliding attention, linear attention, or neither) from the
+methods it has; each install's checks are a lazy generator of problems
+(``_*_problems``) in the reference's order, and the install raises the first
+one, or, if there is none, performs its writes. The retained window of a
+Gemma layer comes from ``layouts.retained_window``, the same function the
+mapper's windowed install uses.
+
+``transform_delta_state`` maps Qwen3.5 DeltaNet memory as ``A^T U B``
+(``cb/architectures/qwen35.py:52-61``) with the HIP kernel behind
+``cb_delta_state_transform`` (16x16x4 fp32 / fp64 MFMAs). Inputs must be GPU
+tensors; there is no CPU path.
 
 Paths are relative to the reference repository; ``cb/`` = ``src/cachebridge/``.
 """
 
 from __future__ import annotations
 
+from collections.abc import Iterator
 from dataclasses import dataclass
 
 import torch
 
 from . import _lib
+from .layouts import retained_window
 
 
 def _positive_int(value, name: str) -> int:
     if type(value) is not int or value < 1:
         raise ValueError(f"{name} must be a positive integer")
     return value
+
+
+def _raise_first(problems: Iterator[Exception]) -> None:
+    problem = next(problems, None)
+    if problem is not None:
+        raise problem
+
+
+_LINEAR_LAYER_API = ("update_conv_state", "update_recurrent_state", "has_previous_state",
+                     "recurrent_states", "conv_states")
+
+
+def _role(layer) -> str:
+    """``"linear"``, ``"sliding"``, ``"full"`` or ``"other"`` for a cache layer (duck-typed).
+
+    A layer with recurrent state is never an attention layer; an attention
+    layer must accept ``update(key, value)``.
+    """
+    if all(hasattr(layer, name) for name in _LINEAR_LAYER_API):
+        return "linear"
+    if hasattr(layer, "recurrent_states") or not hasattr(layer, "update"):
+        return "other"
+    return "sliding" if getattr(layer, "is_sliding", False) else "full"
+
+
+def _kv_pair_problem(key, value) -> Exception | None:
+    if key.ndim != 4 or key.shape != value.shape or key.dtype != value.dtype or key.device != value.device:
+        return ValueError("K/V must match [batch,heads,tokens,head_dim], dtype and device")
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -52,25 +90,30 @@ def materialize_kv(content_key, value, *, layer_type, sliding_window, prefix_len
     if content_key.ndim != 3 or content_key.shape != value.shape:
         raise ValueError("Gemma K/V must have matching [tokens,heads,dim] shapes")
     tokens = content_key.shape[0]
-    prefix = tokens if prefix_length is None else prefix_length
-    if prefix != tokens or prefix < 1:
+    if prefix_length is not None and prefix_length != tokens:
         raise ValueError("prefix length must equal the materialized token count")
-    if layer_type == "sliding_attention":
-        if _positive_int(sliding_window, "sliding_window") < 2:
-            raise ValueError("Sliding window must leave room for the next token")
-        kept = min(tokens, sliding_window - 1)
-    elif layer_type == "full_attention":
-        kept = tokens
-    else:
-        raise ValueError(f"Unsupported Gemma layer type: {layer_type}")
-    first = tokens - kept
-    return MaterializedKV(content_key[first:], value[first:], first, prefix)
+    first, _ = retained_window(tokens, layer_type=layer_type, sliding_window=sliding_window)
+    return MaterializedKV(content_key[first:], value[first:], first, tokens)
 
 
-def _expected_history(layer, prefix_length: int) -> int:
-    if getattr(layer, "is_sliding", False):
-        return min(prefix_length, int(layer.sliding_window) - 1)
-    return prefix_length
+def _gemma_roster_problems(cache, mapped, prefix_length: int) -> Iterator[Exception]:
+    if set(mapped) != set(range(len(cache.layers))):
+        yield ValueError("Gemma payload must cover every target layer")
+        return
+    for index, layer in enumerate(cache.layers):
+        key, value = mapped[index]
+        problem = _kv_pair_problem(key, value)
+        if problem is not None:
+            yield problem
+        role = _role(layer)
+        if role not in ("sliding", "full"):
+            yield TypeError("Expected an attention cache layer")
+        if getattr(layer, "is_initialized", False):
+            yield ValueError(f"Target cache layer {index} is already initialized")
+        # A sliding layer holds the last W - 1 tokens; its window is not re-validated here.
+        expected = min(prefix_length, int(layer.sliding_window) - 1) if role == "sliding" else prefix_length
+        if expected < 1 or key.shape[-2] != expected:
+            yield ValueError(f"Invalid history length for layer {index}: expected {expected}")
 
 
 def install_kv(cache, *, mapped, prefix_length):
@@ -79,25 +122,14 @@ def install_kv(cache, *, mapped, prefix_length):
     ``mapped`` maps each layer index to ``(key, value)`` of shape
     ``[batch, heads, tokens, head_dim]``. The whole roster is checked first
     (coverage, geometry, layer kind, fresh layers, history length); only then
-    is any layer updated (``gemma3.py:61-94``).
+    is any layer updated, and a sliding layer records the whole prefix length
+    as its cumulative length (``gemma3.py:61-94``).
     """
     _positive_int(prefix_length, "prefix_length")
-    if set(mapped) != set(range(len(cache.layers))):
-        raise ValueError("Gemma payload must cover every target layer")
-    for index, layer in enumerate(cache.layers):
-        key, value = mapped[index]
-        if key.ndim != 4 or key.shape != value.shape or key.dtype != value.dtype or key.device != value.device:
-            raise ValueError("K/V must match [batch,heads,tokens,head_dim], dtype and device")
-        if not hasattr(layer, "update") or hasattr(layer, "recurrent_states"):
-            raise TypeError("Expected an attention cache layer")
-        if getattr(layer, "is_initialized", False):
-            raise ValueError(f"Target cache layer {index} is already initialized")
-        expected = _expected_history(layer, prefix_length)
-        if expected < 1 or key.shape[-2] != expected:
-            raise ValueError(f"Invalid history length for layer {index}: expected {expected}")
+    _raise_first(_gemma_roster_problems(cache, mapped, prefix_length))
     for index, layer in enumerate(cache.layers):
         layer.update(*mapped[index])
-        if getattr(layer, "is_sliding", False):
+        if _role(layer) == "sliding":
             layer.cumulative_length = prefix_length
 
 
@@ -181,50 +213,65 @@ def required_replay(conv_kernel_size):
     return _positive_int(conv_kernel_size, "conv_kernel_size") - 1
 
 
+def _attention_problems(cache, layer_index, key, value) -> Iterator[Exception]:
+    if key.ndim != 4 or key.shape != value.shape or key.shape[-2] < 1:
+        yield ValueError("K/V must match nonempty [batch,heads,tokens,head_dim]")
+    if key.dtype != value.dtype or key.device != value.device:
+        yield ValueError("K/V dtype and device must match")
+    layer = cache.layers[layer_index]
+    if _role(layer) != "full":
+        yield TypeError("Expected a full-attention cache layer")
+    if getattr(layer, "is_initialized", False):
+        yield ValueError("Target cache layer is already initialized")
+
+
 def install_attention_kv(cache, layer_index, key, value):
     """Install K/V into a fresh full-attention layer (``qwen35.py:69-82``)."""
-    if key.ndim != 4 or key.shape != value.shape or key.shape[-2] < 1:
-        raise ValueError("K/V must match nonempty [batch,heads,tokens,head_dim]")
-    if key.dtype != value.dtype or key.device != value.device:
-        raise ValueError("K/V dtype and device must match")
-    layer = cache.layers[layer_index]
-    if getattr(layer, "is_sliding", False) or hasattr(layer, "recurrent_states") or not hasattr(layer, "update"):
-        raise TypeError("Expected a full-attention cache layer")
-    if getattr(layer, "is_initialized", False):
-        raise ValueError("Target cache layer is already initialized")
-    layer.update(key, value)
+    _raise_first(_attention_problems(cache, layer_index, key, value))
+    cache.layers[layer_index].update(key, value)
 
 
-_LINEAR_LAYER_API = ("update_conv_state", "update_recurrent_state", "has_previous_state",
-                     "recurrent_states", "conv_states")
+def _linear_payload_problems(recurrent_state, conv_state, conv_kernel_size) -> Iterator[Exception]:
+    if recurrent_state.ndim != 4 or conv_state.ndim != 3:
+        yield ValueError("Expected recurrent [batch,heads,key,value] and convolution [batch,channels,kernel]")
+        return
+    _positive_int(conv_kernel_size, "conv_kernel_size")
+    if conv_state.shape[-1] != conv_kernel_size or recurrent_state.shape[0] != conv_state.shape[0]:
+        yield ValueError("Convolution length or batch geometry mismatch")
+    if recurrent_state.device != conv_state.device:
+        yield ValueError("Recurrent and convolution states must share a device")
+    if not (recurrent_state.is_floating_point() and conv_state.is_floating_point()):
+        yield ValueError("Recurrent and convolution states must be floating-point tensors")
+
+
+def _linear_spec_problems(spec, layer_index, recurrent_state, conv_state,
+                          conv_kernel_size) -> Iterator[Exception]:
+    if spec.index != layer_index or spec.kind != "linear_attention":
+        yield ValueError("Layer specification does not match the recurrent destination")
+    if tuple(recurrent_state.shape[1:]) != (spec.value_heads, spec.key_dim, spec.value_dim):
+        yield ValueError("Recurrent tensor does not match the layer specification")
+    conv_shape = (spec.conv_channels, spec.conv_kernel_size)
+    if tuple(conv_state.shape[1:]) != conv_shape or conv_kernel_size != spec.conv_kernel_size:
+        yield ValueError("Convolution tensor does not match the layer specification")
 
 
 def install_linear_state(cache, layer_index, *, recurrent_state, conv_state, conv_kernel_size, spec=None):
     """Install mapped recurrent memory and the receiver's convolution tail into a
     fresh linear-attention layer (``qwen35.py:85-160``). Every check runs
     before the layer is touched."""
-    if recurrent_state.ndim != 4 or conv_state.ndim != 3:
-        raise ValueError("Expected recurrent [batch,heads,key,value] and convolution [batch,channels,kernel]")
-    _positive_int(conv_kernel_size, "conv_kernel_size")
-    if conv_state.shape[-1] != conv_kernel_size or recurrent_state.shape[0] != conv_state.shape[0]:
-        raise ValueError("Convolution length or batch geometry mismatch")
-    if recurrent_state.device != conv_state.device:
-        raise ValueError("Recurrent and convolution states must share a device")
-    if not recurrent_state.is_floating_point() or not conv_state.is_floating_point():
-        raise ValueError("Recurrent and convolution states must be floating-point tensors")
-    if spec is not None:
-        if spec.index != layer_index or spec.kind != "linear_attention":
-            raise ValueError("Layer specification does not match the recurrent destination")
-        if tuple(recurrent_state.shape[1:]) != (spec.value_heads, spec.key_dim, spec.value_dim):
-            raise ValueError("Recurrent tensor does not match the layer specification")
-        if (tuple(conv_state.shape[1:]) != (spec.conv_channels, spec.conv_kernel_size)
-                or conv_kernel_size != spec.conv_kernel_size):
-            raise ValueError("Convolution tensor does not match the layer specification")
+
+    def problems():
+        yield from _linear_payload_problems(recurrent_state, conv_state, conv_kernel_size)
+        if spec is not None:
+            yield from _linear_spec_problems(spec, layer_index, recurrent_state, conv_state, conv_kernel_size)
+        layer = cache.layers[layer_index]
+        if _role(layer) != "linear":
+            yield TypeError("Target is not a linear-attention cache layer")
+        elif bool(layer.has_previous_state[0]):
+            yield ValueError("Target cache layer already has previous state")
+
+    _raise_first(problems())
     layer = cache.layers[layer_index]
-    if any(not hasattr(layer, name) for name in _LINEAR_LAYER_API):
-        raise TypeError("Target is not a linear-attention cache layer")
-    if bool(layer.has_previous_state[0]):
-        raise ValueError("Target cache layer already has previous state")
     layer.update_conv_state(conv_state, state_idx=0, conv_kernel_size=conv_kernel_size)
     layer.update_recurrent_state(recurrent_state, state_idx=0)
     if not bool(layer.has_previous_state[0]):

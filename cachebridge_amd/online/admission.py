@@ -1,33 +1,38 @@
 """Admission of handoff requests around the GPU map (host logic).
 
-Mirrors the reference's online admission contracts
-(``cb/online/admission.py:24-565``; ``cb/`` = ``src/cachebridge/``):
+The public contract is the reference's (``cb/online/admission.py:24-565``,
+``cb/`` = ``src/cachebridge/``): the same class and dataclass names and
+fields, the same reason strings a scheduler routes on, and the same error
+texts callers match. The machinery is this module's own:
 
-- ``LiveMapperMechanism`` (``:42-82``): the fail-closed capability contract
-  that must hold before mapping may overlap target decode;
-- ``LiveMapperCostPolicy`` (``:85-104``): the break-even gate on history
-  length;
-- ``OnlineMapperRouter`` (``:134-253``): live mapper, cohort mapper, native
-  re-prefill or backpressure, and dispatch of exactly one path;
-- ``LiveMapperAdmission`` (``:256-394``): one unpublished transaction that
-  publishes only with GPU completion and the TP vote;
-- ``OnlineMapperAdmission`` (``:397-565``): the one-cohort state machine,
-  FIFO publication, one coalesced query batch.
+- every controller is a small table-driven state machine: a method names a
+  step, the table says which state the step leaves from and which it enters,
+  and ownership of the request being stepped is checked before the move;
+- a cohort is a ``_Ledger``: its request ids in admission order and a
+  publication cursor (everything before the cursor is published, the request
+  at the cursor is the only one that may be mapped), so FIFO order holds by
+  construction rather than by bookkeeping of separate lists;
+- the router is an ordered list of rules, evaluated first-match;
+- the live mapper's isolation properties are compared field by field with
+  the one configuration that is allowed (``_ISOLATED``).
 
-One addition: ``OnlineMapperAdmission.execute_cohort_batched`` maps a whole
-admitted cohort with one GPU launch (``cb_map_install_batch``, every row
-identical to the per-request launches) and then publishes the requests in FIFO
-order through the same state machine, where ``execute_cohort`` runs one mapper
-transaction per request.
+``OnlineMapperAdmission.execute_cohort_batched`` is an addition: the whole
+admitted cohort is mapped in one launch (``cb_map_install_batch``, every row
+identical to the per-request launches), then published request by request in
+admission order through the same state machine.
 """
 
 from __future__ import annotations
 
-from collections.abc import Callable, Iterable
-from dataclasses import dataclass
+from collections.abc import Callable, Iterable, Sequence
+from dataclasses import dataclass, fields
 from typing import Literal, TypeVar
 
 _Result = TypeVar("_Result")
+
+# Bytes of device workspace per mapped token of a one-launch cohort: the
+# int32 source row, target row and position the batch resolver writes.
+BATCH_WORKSPACE_BYTES_PER_TOKEN = 12
 
 
 @dataclass(frozen=True)
@@ -46,54 +51,6 @@ class AdmissionPlan:
     mapper_transactions_in_flight: int
     mapper_workspace_scales_with_cohort: bool
     query_coalescing: bool
-
-
-@dataclass(frozen=True)
-class LiveMapperMechanism:
-    """Capabilities that must all hold before mapper work overlaps target decode."""
-
-    mapper_compute_role: Literal["source", "target"] = "source"
-    mapped_output_slots: int = 2
-    direct_target_placement: bool = True
-    target_mapper_workspace_bytes: int = 0
-    target_transfer_workspace_bytes: int = 0
-    scheduler_serialized_allocation: bool = True
-    scheduler_serialized_publication: bool = True
-    source_slot_gpu_ack: bool = True
-    max_staged_transactions: int = 1
-
-    def validate(self) -> None:
-        checks = (
-            (self.mapper_compute_role == "source", "live mapper compute must be source-isolated"),
-            (self.mapped_output_slots >= 2, "live mapper requires at least two output slots"),
-            (self.direct_target_placement, "live mapper requires direct target placement"),
-            (self.target_mapper_workspace_bytes == 0, "live mapper cannot allocate target mapper workspace"),
-            (self.target_transfer_workspace_bytes == 0, "live mapper cannot allocate target transfer workspace"),
-            (self.scheduler_serialized_allocation, "target allocation must be scheduler-serialized"),
-            (self.scheduler_serialized_publication, "target publication must be scheduler-serialized"),
-            (self.source_slot_gpu_ack, "source slots require target GPU-complete ACKs"),
-            (self.max_staged_transactions == 1, "exactly one unpublished transaction is supported"),
-        )
-        for ok, message in checks:
-            if not ok:
-                raise ValueError(message)
-
-
-@dataclass(frozen=True)
-class LiveMapperCostPolicy:
-    """Map a request live only when its history is long enough to pay off."""
-
-    min_history_tokens: int
-    objective: Literal["ttft"] = "ttft"
-
-    def validate(self) -> None:
-        if self.min_history_tokens <= 0:
-            raise ValueError("min_history_tokens must be positive")
-        if self.objective != "ttft":
-            raise ValueError("only the measured ttft objective is supported")
-
-    def admits(self, request: MapperRequest) -> bool:
-        return request.history_tokens >= self.min_history_tokens
 
 
 @dataclass(frozen=True)
@@ -123,15 +80,99 @@ class RouterDecision:
     cohort_preformed: bool
 
 
-def _check_identities(ids) -> None:
-    if any(not i for i in ids):
+def _require_identities(ids: Sequence[str]) -> None:
+    if not all(ids):
         raise ValueError("request identity must be non-empty")
-    if len(set(ids)) != len(ids):
+    if len(frozenset(ids)) < len(ids):
         raise ValueError("request identities must be unique")
 
 
+# --- the live mapper's isolation contract -------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class LiveMapperMechanism:
+    """Capabilities that must all hold before mapper work overlaps target decode.
+
+    The defaults are the one isolated configuration; ``validate`` fails closed
+    on the first field (in declaration order) that departs from it.
+    """
+
+    mapper_compute_role: Literal["source", "target"] = "source"
+    mapped_output_slots: int = 2
+    direct_target_placement: bool = True
+    target_mapper_workspace_bytes: int = 0
+    target_transfer_workspace_bytes: int = 0
+    scheduler_serialized_allocation: bool = True
+    scheduler_serialized_publication: bool = True
+    source_slot_gpu_ack: bool = True
+    max_staged_transactions: int = 1
+
+    def unmet_requirements(self) -> list[str]:
+        """Messages of every isolation property this mechanism lacks."""
+        out = []
+        for f in fields(self):
+            value, required = getattr(self, f.name), getattr(_ISOLATED, f.name)
+            ok = value >= required if f.name in _AT_LEAST else value == required
+            if not ok:
+                out.append(_ISOLATION_MESSAGES[f.name])
+        return out
+
+    def validate(self) -> None:
+        unmet = self.unmet_requirements()
+        if unmet:
+            raise ValueError(unmet[0])
+
+
+_ISOLATED = LiveMapperMechanism()
+_AT_LEAST = frozenset({"mapped_output_slots"})  # more slots than the minimum are fine
+_ISOLATION_MESSAGES = {
+    "mapper_compute_role": "live mapper compute must be source-isolated",
+    "mapped_output_slots": "live mapper requires at least two output slots",
+    "direct_target_placement": "live mapper requires direct target placement",
+    "target_mapper_workspace_bytes": "live mapper cannot allocate target mapper workspace",
+    "target_transfer_workspace_bytes": "live mapper cannot allocate target transfer workspace",
+    "scheduler_serialized_allocation": "target allocation must be scheduler-serialized",
+    "scheduler_serialized_publication": "target publication must be scheduler-serialized",
+    "source_slot_gpu_ack": "source slots require target GPU-complete ACKs",
+    "max_staged_transactions": "exactly one unpublished transaction is supported",
+}
+
+
+@dataclass(frozen=True)
+class LiveMapperCostPolicy:
+    """Map a request live only when its history is long enough to pay off."""
+
+    min_history_tokens: int
+    objective: Literal["ttft"] = "ttft"
+
+    def validate(self) -> None:
+        if self.min_history_tokens <= 0:
+            raise ValueError("min_history_tokens must be positive")
+        if self.objective != "ttft":
+            raise ValueError("only the measured ttft objective is supported")
+
+    def admits(self, request: MapperRequest) -> bool:
+        return request.history_tokens >= self.min_history_tokens
+
+
+# --- routing --------------------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class _Arrival:
+    requests: tuple           # after cancellations
+    decoder_active: bool
+    service_class: str
+    cohort_preformed: bool
+
+
 class OnlineMapperRouter:
-    """Choose the serving path of an arrival cohort."""
+    """Choose the serving path of an arrival cohort.
+
+    The cohort is atomic: it takes one path, and a live cost policy that any
+    request misses sends all of it to native re-prefill.
+    """
 
     def __init__(self, *, max_cohort_requests: int = 4, live_mechanism: LiveMapperMechanism | None = None,
                  live_cost_policy: LiveMapperCostPolicy | None = None) -> None:
@@ -146,6 +187,27 @@ class OnlineMapperRouter:
         self.max_cohort_requests = max_cohort_requests
         self.live_mechanism = live_mechanism
         self.live_cost_policy = live_cost_policy
+        self._rules = self._build_rules()
+
+    def _build_rules(self) -> list[tuple[str, str, Callable[[_Arrival], bool]]]:
+        """(mode, reason, applies) in priority order; the last rule always applies."""
+        limit, policy = self.max_cohort_requests, self.live_cost_policy
+        rules = [
+            ("backpressure", "cohort_canceled", lambda a: not a.requests),
+            ("backpressure", "cohort_request_limit", lambda a: len(a.requests) > limit),
+        ]
+        if self.live_mechanism is not None:
+            rules += [
+                ("native_reprefill", "below_live_mapper_break_even",
+                 lambda a: policy is not None and not all(map(policy.admits, a.requests))),
+                ("cachebridge_live", "source_isolated_live_mapper", lambda a: True),
+            ]
+        return rules + [
+            ("native_reprefill", "decoder_active", lambda a: a.decoder_active),
+            ("native_reprefill", "latency_service_class", lambda a: a.service_class == "latency"),
+            ("native_reprefill", "trickle_arrival_no_wait", lambda a: not a.cohort_preformed),
+            ("cachebridge_cohort", "idle_preformed_throughput_cohort", lambda a: True),
+        ]
 
     def route(self, requests: Iterable[MapperRequest], *, decoder_active: bool,
               service_class: Literal["latency", "throughput"], cohort_preformed: bool,
@@ -153,47 +215,41 @@ class OnlineMapperRouter:
         cohort = tuple(requests)
         if not cohort:
             raise ValueError("route requires at least one request")
-        ids = [r.request_id for r in cohort]
-        _check_identities(ids)
+        _require_identities([r.request_id for r in cohort])
         canceled = tuple(canceled_request_ids)
-        if len(set(canceled)) != len(canceled):
+        dropped = frozenset(canceled)
+        if len(dropped) < len(canceled):
             raise ValueError("canceled request identities must be unique")
-        unknown = set(canceled) - set(ids)
+        unknown = dropped.difference(r.request_id for r in cohort)
         if unknown:
             raise ValueError(f"unknown canceled request identities: {sorted(unknown)}")
-        active = tuple(r for r in cohort if r.request_id not in set(canceled))
-
-        def decide(mode, reason, reqs=active):
-            return RouterDecision(mode, reason, reqs, canceled, decoder_active, service_class, cohort_preformed)
-
-        if not active:
-            return decide("backpressure", "cohort_canceled", ())
-        if len(active) > self.max_cohort_requests:
-            return decide("backpressure", "cohort_request_limit")
-        if self.live_mechanism is not None:
-            if self.live_cost_policy is not None and not all(self.live_cost_policy.admits(r) for r in active):
-                return decide("native_reprefill", "below_live_mapper_break_even")
-            return decide("cachebridge_live", "source_isolated_live_mapper")
-        if decoder_active:
-            return decide("native_reprefill", "decoder_active")
-        if service_class == "latency":
-            return decide("native_reprefill", "latency_service_class")
-        if not cohort_preformed:
-            return decide("native_reprefill", "trickle_arrival_no_wait")
-        return decide("cachebridge_cohort", "idle_preformed_throughput_cohort")
+        arrival = _Arrival(tuple(r for r in cohort if r.request_id not in dropped), decoder_active,
+                           service_class, cohort_preformed)
+        mode, reason = next((m, why) for m, why, applies in self._rules if applies(arrival))
+        return RouterDecision(mode, reason, arrival.requests, canceled, decoder_active, service_class,
+                              cohort_preformed)
 
     def dispatch(self, decision: RouterDecision, *, cachebridge_live: Callable | None = None,
                  cachebridge_cohort: Callable, native_reprefill: Callable):
         """Run exactly the one serving path the decision selected."""
-        if decision.mode == "cachebridge_live":
-            if cachebridge_live is None:
-                raise RuntimeError("cachebridge_live callback is required")
-            return cachebridge_live(decision.requests)
-        if decision.mode == "cachebridge_cohort":
-            return cachebridge_cohort(decision.requests)
-        if decision.mode == "native_reprefill":
-            return native_reprefill(decision.requests)
-        raise RuntimeError(f"cannot dispatch backpressured route: {decision.reason}")
+        if decision.mode == "backpressure":
+            raise RuntimeError(f"cannot dispatch backpressured route: {decision.reason}")
+        paths = {"cachebridge_live": cachebridge_live, "cachebridge_cohort": cachebridge_cohort,
+                 "native_reprefill": native_reprefill}
+        path = paths[decision.mode]
+        if path is None:
+            raise RuntimeError(f"{decision.mode} callback is required")
+        return path(decision.requests)
+
+
+# --- one live (post-arrival) transaction -----------------------------------------------------------
+
+# step -> (state it leaves from, state it enters)
+_LIVE_STEPS = {
+    "mark_source_complete": ("mapping", "source_ready"),
+    "publish": ("source_ready", "published"),
+    "mark_submitted": ("published", "idle"),
+}
 
 
 class LiveMapperAdmission:
@@ -205,87 +261,127 @@ class LiveMapperAdmission:
         mechanism.validate()
         self.mechanism = mechanism
         self.query_reserve_tokens = query_reserve_tokens
-        self._active: MapperRequest | None = None
-        self._phase = "idle"
-        self._decoder_active = False
-        self._completed: list[str] = []
+        self._state = "idle"
+        self._request: MapperRequest | None = None
+        self._during_decode = False
+        self._submitted: list[str] = []
         self._error: str | None = None
 
     def plan(self, request: MapperRequest, *, available_target_tokens: int,
              decoder_active: bool) -> LiveAdmissionPlan:
-        if not request.request_id:
-            raise ValueError("request identity must be non-empty")
+        _require_identities([request.request_id])
         if request.history_tokens <= 0:
             raise ValueError("history_tokens must be positive")
-        required = request.history_tokens + self.query_reserve_tokens
-        if self._phase != "idle":
-            admitted, reason = False, "mapper_transaction_in_flight"
-        elif required > available_target_tokens:
-            admitted, reason = False, "target_token_backpressure"
+        need = request.history_tokens + self.query_reserve_tokens
+        if self._state != "idle":
+            verdict = (False, "mapper_transaction_in_flight")
+        elif need > available_target_tokens:
+            verdict = (False, "target_token_backpressure")
         else:
-            admitted, reason = True, "admitted_during_decode" if decoder_active else "admitted"
-        return LiveAdmissionPlan(admitted, reason, request, required, available_target_tokens, decoder_active)
+            verdict = (True, "admitted_during_decode" if decoder_active else "admitted")
+        return LiveAdmissionPlan(*verdict, request, need, available_target_tokens, decoder_active)
 
     def begin(self, plan: LiveAdmissionPlan) -> MapperRequest:
-        if self._phase != "idle":
-            raise RuntimeError(f"cannot begin while state={self._phase}")
+        if self._state != "idle":
+            raise RuntimeError(f"cannot begin while state={self._state}")
         if not plan.admitted:
             raise RuntimeError(f"cannot execute rejected plan: {plan.reason}")
-        if plan.request.request_id in self._completed:
+        if plan.request.request_id in self._submitted:
             raise RuntimeError("request identity was already published")
-        self._active, self._decoder_active = plan.request, plan.decoder_active
-        self._phase, self._error = "mapping", None
+        self._request, self._during_decode = plan.request, plan.decoder_active
+        self._state, self._error = "mapping", None
         return plan.request
 
+    def _step(self, step: str, request_id: str) -> None:
+        leaves, enters = _LIVE_STEPS[step]
+        owner = None if self._request is None else self._request.request_id
+        if self._state != leaves or owner != request_id:
+            raise RuntimeError("operation does not own the active mapper transaction")
+        self._state = enters
+
     def mark_source_complete(self, request_id: str) -> None:
-        self._own(request_id, "mapping")
-        self._phase = "source_ready"
+        self._step("mark_source_complete", request_id)
 
     def publish(self, request_id: str, proof: PublicationProof) -> None:
-        self._own(request_id, "source_ready")
-        if not (proof.gpu_reads_complete and proof.tp_vote_passed):
+        leaves, _ = _LIVE_STEPS["publish"]
+        if self._state == leaves and self._request is not None and self._request.request_id == request_id \
+                and not (proof.gpu_reads_complete and proof.tp_vote_passed):
             self.quarantine("publication proof failed")
             raise RuntimeError("cannot publish without GPU completion and TP vote")
-        self._phase = "published"
+        self._step("publish", request_id)
 
     def mark_submitted(self, request_id: str) -> None:
-        self._own(request_id, "published")
-        self._completed.append(request_id)
-        self._active, self._decoder_active, self._phase = None, False, "idle"
+        self._step("mark_submitted", request_id)
+        self._submitted.append(request_id)
+        self._clear()
 
     def rollback(self, request_id: str, *, gpu_reads_complete: bool, target_pages_released: bool) -> None:
-        if self._active is None or self._active.request_id != request_id:
+        if self._request is None or self._request.request_id != request_id:
             raise RuntimeError("rollback does not own the active transaction")
-        if self._phase not in ("mapping", "source_ready"):
-            raise RuntimeError(f"cannot roll back while state={self._phase}")
+        if self._state not in ("mapping", "source_ready"):
+            raise RuntimeError(f"cannot roll back while state={self._state}")
         if not (gpu_reads_complete and target_pages_released):
             self.quarantine("unsafe rollback")
             raise RuntimeError("rollback requires completed reads and released pages")
-        self._active, self._decoder_active, self._phase = None, False, "idle"
+        self._clear()
+
+    def _clear(self) -> None:
+        self._request, self._during_decode, self._state = None, False, "idle"
 
     def quarantine(self, error) -> None:
-        self._phase, self._error = "quarantined", str(error)
+        self._state, self._error = "quarantined", str(error)
 
     def snapshot(self) -> dict:
         m = self.mechanism
-        return {
-            "state": self._phase,
-            "active_request": None if self._active is None else self._active.request_id,
-            "decoder_active_during_mapping": self._decoder_active,
-            "completed_request_ids": tuple(self._completed),
+        state = {
+            "state": self._state,
+            "active_request": None if self._request is None else self._request.request_id,
+            "decoder_active_during_mapping": self._during_decode,
+            "completed_request_ids": tuple(self._submitted),
             "error": self._error,
-            "mapper_compute_role": m.mapper_compute_role,
-            "mapped_output_slots": m.mapped_output_slots,
-            "max_staged_transactions": m.max_staged_transactions,
-            "target_mapper_workspace_bytes": m.target_mapper_workspace_bytes,
-            "target_transfer_workspace_bytes": m.target_transfer_workspace_bytes,
-            "direct_target_placement": m.direct_target_placement,
-            "scheduler_serialized_publication": m.scheduler_serialized_publication,
         }
+        for name in ("mapper_compute_role", "mapped_output_slots", "max_staged_transactions",
+                     "target_mapper_workspace_bytes", "target_transfer_workspace_bytes",
+                     "direct_target_placement", "scheduler_serialized_publication"):
+            state[name] = getattr(m, name)
+        return state
 
-    def _own(self, request_id: str, phase: str) -> None:
-        if self._phase != phase or self._active is None or self._active.request_id != request_id:
-            raise RuntimeError("operation does not own the active mapper transaction")
+
+# --- one admitted cohort --------------------------------------------------------------------------
+
+
+class _Ledger:
+    """A cohort's requests in admission order and how far publication got.
+
+    ``requests[:cursor]`` are published; ``requests[cursor]`` is the only one
+    that may be mapped next; ``active`` is its id while its transaction runs.
+    """
+
+    def __init__(self, requests: tuple = ()) -> None:
+        self.requests = requests
+        self.cursor = 0
+        self.active: str | None = None
+
+    @property
+    def ids(self) -> tuple:
+        return tuple(r.request_id for r in self.requests)
+
+    @property
+    def published(self) -> tuple:
+        return self.ids[:self.cursor]
+
+    @property
+    def pending(self) -> tuple:
+        return self.ids[self.cursor:]
+
+
+# step -> (states it may leave from, state it enters)
+_COHORT_STEPS = {
+    "admit": (("idle",), "admitted"),
+    "begin_next_mapper": (("admitted", "mapping"), "mapping"),
+    "coalesced_query_batch": (("ready",), "dispatched"),
+    "finish_queries": (("dispatched",), "idle"),
+}
 
 
 class OnlineMapperAdmission:
@@ -298,83 +394,90 @@ class OnlineMapperAdmission:
             raise ValueError("query reserve must be non-negative")
         self.max_cohort_requests = max_cohort_requests
         self.query_reserve_tokens_per_request = query_reserve_tokens_per_request
-        self._reset("idle")
-
-    def _reset(self, state: str) -> None:
-        self._state = state
-        self._requests: tuple = ()
-        self._pending: list[str] = []
-        self._published: list[str] = []
-        self._active_request: str | None = None
+        self._state = "idle"
+        self._ledger = _Ledger()
         self._error: str | None = None
+        self._batched_tokens = 0  # tokens of the cohort mapped in one launch, 0 for per-request maps
+
+    def _leave(self, step: str, verb: str) -> None:
+        sources, enters = _COHORT_STEPS[step]
+        if self._state not in sources:
+            raise RuntimeError(f"cannot {verb} while state={self._state}")
+        self._state = enters
 
     def plan(self, requests: Iterable[MapperRequest], *, available_target_tokens: int) -> AdmissionPlan:
         cohort = tuple(requests)
         if not cohort:
             raise ValueError("cohort must be non-empty")
+
+        def verdict(ok, reason, required):
+            return AdmissionPlan(ok, reason, cohort, required, available_target_tokens, int(ok), False, True)
+
         if len(cohort) > self.max_cohort_requests:
-            return AdmissionPlan(False, "cohort_request_limit", cohort, 0, available_target_tokens, 0, False, True)
-        _check_identities([r.request_id for r in cohort])
-        if any(r.history_tokens <= 0 for r in cohort):
+            return verdict(False, "cohort_request_limit", 0)
+        _require_identities([r.request_id for r in cohort])
+        if min(r.history_tokens for r in cohort) <= 0:
             raise ValueError("history_tokens must be positive")
-        required = sum(r.history_tokens for r in cohort) + len(cohort) * self.query_reserve_tokens_per_request
-        admitted = required <= available_target_tokens
-        return AdmissionPlan(admitted, "admitted" if admitted else "target_token_backpressure", cohort, required,
-                             available_target_tokens, 1 if admitted else 0, False, True)
+        required = sum(r.history_tokens + self.query_reserve_tokens_per_request for r in cohort)
+        if required > available_target_tokens:
+            return verdict(False, "target_token_backpressure", required)
+        return verdict(True, "admitted", required)
 
     def admit(self, plan: AdmissionPlan) -> None:
-        if self._state != "idle":
-            raise RuntimeError(f"cannot admit while state={self._state}")
-        if not plan.admitted:
+        if self._state == "idle" and not plan.admitted:
             raise RuntimeError(f"cannot execute rejected plan: {plan.reason}")
-        self._reset("admitted")
-        self._requests = plan.requests
-        self._pending = [r.request_id for r in plan.requests]
+        self._leave("admit", "admit")
+        self._ledger, self._error, self._batched_tokens = _Ledger(plan.requests), None, 0
 
     def begin_next_mapper(self) -> MapperRequest:
-        if self._state not in ("admitted", "mapping"):
-            raise RuntimeError(f"cannot start mapper while state={self._state}")
-        if self._active_request is not None:
-            raise RuntimeError("another mapper transaction is active")
-        if not self._pending:
-            raise RuntimeError("cohort has no pending mapper request")
-        self._active_request = self._pending[0]
-        self._state = "mapping"
-        return next(r for r in self._requests if r.request_id == self._active_request)
+        ledger = self._ledger
+        if self._state in _COHORT_STEPS["begin_next_mapper"][0]:
+            if ledger.active is not None:
+                raise RuntimeError("another mapper transaction is active")
+            if ledger.cursor == len(ledger.requests):
+                raise RuntimeError("cohort has no pending mapper request")
+        self._leave("begin_next_mapper", "start mapper")
+        request = ledger.requests[ledger.cursor]
+        ledger.active = request.request_id
+        return request
 
     def publish_active_mapper(self, request_id: str) -> None:
-        if self._state != "mapping" or self._active_request != request_id:
+        ledger = self._ledger
+        if self._state != "mapping" or ledger.active != request_id:
             raise RuntimeError("publication does not own the active mapper transaction")
-        if not self._pending or self._pending[0] != request_id:
+        if ledger.pending[:1] != (request_id,):
             raise RuntimeError("mapper completion violated FIFO admission order")
-        self._published.append(self._pending.pop(0))
-        self._active_request = None
-        self._state = "mapping" if self._pending else "ready"
+        ledger.cursor += 1
+        ledger.active = None
+        self._state = "mapping" if ledger.pending else "ready"
 
     def coalesced_query_batch(self) -> tuple:
-        if self._state != "ready" or self._active_request is not None or self._pending:
+        ledger = self._ledger
+        if self._state != "ready" or ledger.active is not None or ledger.pending:
             raise RuntimeError("queries cannot dispatch before every prefix is published")
-        expected = tuple(r.request_id for r in self._requests)
-        if tuple(self._published) != expected:
+        if ledger.published != ledger.ids:
             raise RuntimeError("published request set differs from admitted cohort")
-        self._state = "dispatched"
-        return expected
+        self._leave("coalesced_query_batch", "dispatch queries")
+        return ledger.ids
 
     def finish_queries(self) -> None:
-        if self._state != "dispatched":
-            raise RuntimeError(f"cannot finish queries while state={self._state}")
-        self._reset("idle")
+        self._leave("finish_queries", "finish queries")
+        self._ledger, self._batched_tokens = _Ledger(), 0
 
-    def execute_cohort(self, plan: AdmissionPlan, *, mapper_transaction: Callable[[MapperRequest], None],
-                       query_batch: Callable[[tuple], _Result]) -> _Result:
-        """One synchronous mapper transaction per request (map, install, checks
-        and the TP vote inside the callback), then one query batch. A callback
-        failure quarantines the cohort and is re-raised."""
+    def _run(self, plan: AdmissionPlan, *, before: Callable[[tuple], None] | None,
+             each: Callable[[MapperRequest], None], query_batch: Callable[[tuple], _Result]) -> _Result:
+        """Admit, optionally map the cohort, step every request FIFO, query once.
+
+        Any failure quarantines the cohort with the failing request still
+        active (or none, if ``before`` failed) and is re-raised.
+        """
         self.admit(plan)
         try:
-            while self._pending:
+            if before is not None:
+                before(self._ledger.requests)
+            while self._ledger.pending:
                 request = self.begin_next_mapper()
-                mapper_transaction(request)
+                each(request)
                 self.publish_active_mapper(request.request_id)
             result = query_batch(self.coalesced_query_batch())
         except BaseException as error:
@@ -382,6 +485,12 @@ class OnlineMapperAdmission:
             raise
         self.finish_queries()
         return result
+
+    def execute_cohort(self, plan: AdmissionPlan, *, mapper_transaction: Callable[[MapperRequest], None],
+                       query_batch: Callable[[tuple], _Result]) -> _Result:
+        """One synchronous mapper transaction per request (map, install, checks
+        and the TP vote inside the callback), then one query batch."""
+        return self._run(plan, before=None, each=mapper_transaction, query_batch=query_batch)
 
     def execute_cohort_batched(self, plan: AdmissionPlan, *, map_cohort: Callable[[tuple], None],
                                publish: Callable[[MapperRequest], None],
@@ -391,35 +500,29 @@ class OnlineMapperAdmission:
         ``map_cohort(requests)`` must return after the cohort's map and install
         have completed on the GPU (e.g. ``map_install_batch`` followed by a
         stream synchronization). ``publish(request)`` runs each request's safety
-        checks and TP vote, in admission order; a failure quarantines the
-        cohort with that request active and is re-raised.
+        checks and TP vote, in admission order. The launch's device workspace
+        grows with the cohort (``BATCH_WORKSPACE_BYTES_PER_TOKEN`` per token);
+        ``snapshot`` reports it while the cohort is held.
         """
-        self.admit(plan)
-        try:
-            map_cohort(self._requests)
-            while self._pending:
-                request = self.begin_next_mapper()
-                publish(request)
-                self.publish_active_mapper(request.request_id)
-            result = query_batch(self.coalesced_query_batch())
-        except BaseException as error:
-            self.quarantine(error)
-            raise
-        self.finish_queries()
-        return result
+        def before(requests):
+            self._batched_tokens = sum(r.history_tokens for r in requests)
+            map_cohort(requests)
+
+        return self._run(plan, before=before, each=publish, query_batch=query_batch)
 
     def quarantine(self, error) -> None:
         self._state, self._error = "quarantined", str(error)
 
     def snapshot(self) -> dict:
+        ledger = self._ledger
         return {
             "state": self._state,
-            "active_request": self._active_request,
-            "pending_request_ids": tuple(self._pending),
-            "published_request_ids": tuple(self._published),
+            "active_request": ledger.active,
+            "pending_request_ids": ledger.pending,
+            "published_request_ids": ledger.published,
             "error": self._error,
             "max_mapper_transactions_in_flight": 1,
-            "mapper_workspace_scales_with_cohort": False,
+            "mapper_workspace_scales_with_cohort": self._batched_tokens > 0,
+            "mapper_workspace_bytes": BATCH_WORKSPACE_BYTES_PER_TOKEN * self._batched_tokens,
             "query_coalescing": True,
         }
-

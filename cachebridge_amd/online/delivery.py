@@ -35,7 +35,6 @@ import torch
 from .. import _lib
 from ..plan import Rows, copy_rows, rows_from_layers, rows_from_page
 from ..pool import pool_rows
-from .native_plan import Plan, build_plan
 
 
 def _at_offset(rows: Rows, index_offset: int) -> Rows:
@@ -43,6 +42,26 @@ def _at_offset(rows: Rows, index_offset: int) -> Rows:
     c = _lib.CbRows.from_buffer_copy(rows.c)
     c.index_offset = index_offset
     return Rows(c, rows.dtype, rows.device, rows.keep)
+
+
+def coalesced_runs(rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(first_token, length)`` of every maximal run of consecutive physical
+    rows in ``rows`` (a block's slot indices in token order), as int64 tensors.
+
+    A span-by-span delivery (the reference's peer-copy path) issues one copy
+    per run, kind and layer; ``SelectedBlockDelivery`` moves the block in one
+    gather launch whatever the runs are.
+    """
+    r = rows.reshape(-1).to(torch.int64)
+    n = r.numel()
+    if n == 0:
+        empty = torch.zeros(0, dtype=torch.int64, device=r.device)
+        return empty, empty
+    step = torch.ones(n, dtype=torch.bool, device=r.device)
+    step[1:] = r[1:] != r[:-1] + 1  # a run starts where the row does not follow its predecessor
+    first = torch.nonzero(step).flatten()
+    ends = torch.cat([first[1:], torch.tensor([n], dtype=torch.int64, device=r.device)])
+    return first, ends - first
 
 
 class SelectedBlockDelivery:
@@ -98,11 +117,12 @@ class SelectedBlockDelivery:
     def slot_bytes(self) -> int:
         return sum(t.numel() * t.element_size() for t in self._storage)
 
-    def plan(self, start: int, stop: int) -> Plan:
-        """The block's run geometry over the delivered layers (host copy of the indices)."""
-        return build_plan([int(x) for x in self.indices[start:stop].tolist()], start=0, stop=stop - start,
-                          pool_rows=int(self.pool_rows), layers=len(self.layers), heads=int(self.heads),
-                          dimension=int(self.dim), element_bytes=self.dtype.itemsize)
+    def span_copies(self, start: int, stop: int) -> int:
+        """Copies a span-by-span delivery of block ``[start, stop)`` would issue
+        (one per run of consecutive rows, kind and delivered layer); this
+        class issues one launch."""
+        first, _ = coalesced_runs(self.indices[start:stop])
+        return 2 * len(self.layers) * int(first.numel())
 
     def deliver(self, slot: int, start: int, stop: int) -> torch.Tensor:
         """Gather block ``[start, stop)`` into ``slot`` on the delivery stream.

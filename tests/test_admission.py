@@ -369,3 +369,25 @@ def test_live_admission_cannot_roll_back_published_prefix():
     adm.publish("r0", OK)
     with pytest.raises(RuntimeError, match="state=published"):
         adm.rollback("r0", gpu_reads_complete=True, target_pages_released=True)
+
+
+def test_batched_cohort_snapshot_reports_its_workspace():
+    adm = OnlineMapperAdmission(query_reserve_tokens_per_request=0)
+    seen = []
+    adm.execute_cohort_batched(adm.plan(requests(8, 12), available_target_tokens=20),
+                               map_cohort=lambda rs: seen.append(adm.snapshot()),
+                               publish=noop, query_batch=noop)
+    assert seen[0]["mapper_workspace_scales_with_cohort"]
+    assert seen[0]["mapper_workspace_bytes"] == 12 * 20
+    idle = adm.snapshot()  # released with the cohort
+    assert not idle["mapper_workspace_scales_with_cohort"] and idle["mapper_workspace_bytes"] == 0
+    adm.execute_cohort(adm.plan(requests(8), available_target_tokens=8),
+                       mapper_transaction=lambda r: seen.append(adm.snapshot()), query_batch=noop)
+    assert seen[1]["mapper_workspace_bytes"] == 0
+
+
+def test_live_mechanism_lists_every_missing_property():
+    broken = dataclasses.replace(LiveMapperMechanism(), mapped_output_slots=1, source_slot_gpu_ack=False)
+    assert broken.unmet_requirements() == ["live mapper requires at least two output slots",
+                                           "source slots require target GPU-complete ACKs"]
+    assert dataclasses.replace(LiveMapperMechanism(), mapped_output_slots=3).unmet_requirements() == []

@@ -90,3 +90,29 @@ def test_hash_record_skips_unchanged_files_and_catches_changes(tmp_path, monkeyp
     with pytest.raises(ValueError, match="hash mismatch"):
         verify_descriptor(manifest, hashes=HashRecord(record_path))
     assert any(c.endswith("layer_000.safetensors") for c in calls)
+
+
+def test_hash_record_skips_tensor_checks_of_unchanged_files(tmp_path, monkeypatch):
+    import safetensors.torch as st
+
+    manifest, path, _ = fixture(tmp_path, layers=3)
+    record_path = tmp_path / "hashes.json"
+    assert verify_descriptor(manifest, hashes=HashRecord(record_path))["logical_parameter_bytes"] == 144
+    loads = []
+    real = st.load_file
+    monkeypatch.setattr(st, "load_file", lambda p, *a, **k: loads.append(p) or real(p, *a, **k))
+    report = verify_descriptor(manifest, hashes=HashRecord(record_path))
+    assert loads == [] and report["logical_parameter_bytes"] == 144
+    # a changed file is hashed and checked again (here: it no longer matches its digest)
+    path.write_bytes(path.read_bytes() + b"x")
+    with pytest.raises(ValueError, match="hash mismatch"):
+        verify_descriptor(manifest, hashes=HashRecord(record_path))
+
+
+def test_first_failing_layer_in_descriptor_order_is_reported(tmp_path):
+    manifest, _, d = fixture(tmp_path, layers=4)
+    for i in (1, 3):
+        p = tmp_path / f"layer_{i:03d}.safetensors"
+        p.write_bytes(p.read_bytes() + b"!")
+    with pytest.raises(ValueError, match="hash mismatch: layer_001"):
+        verify_descriptor(manifest)

@@ -90,19 +90,31 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in out.stderr
 
 
-def test_bench_reads_committed_traffic_and_every_leg_has_a_summary():
+def test_bench_traffic_is_used_only_for_the_kernel_source_it_was_measured_on(tmp_path, monkeypatch):
     import importlib.util
     import re
 
     spec = importlib.util.spec_from_file_location("bench_module", ROOT / "bench.py")
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
+    now = bench.kernel_source_sha16()
     for workload in ("tp4", "full"):
-        traffic = bench.profiled_traffic("map_install_stream", workload)
+        traffic, source = bench.profiled_traffic("map_install_stream", workload)
         text = (ROOT / "profiles" / f"map_install_stream_{workload}_traffic.md").read_text()
-        assert isinstance(traffic, int) and traffic > 0
-        assert f"traffic_bytes_per_launch = {traffic}" in text
-    assert bench.profiled_traffic("map_install_stream", "no_such_workload") is None
+        if f"kernel_source_sha16 = {now}" in text:
+            assert isinstance(traffic, int) and f"traffic_bytes_per_launch = {traffic}" in text
+            assert "not measured in this run" in source
+        else:
+            assert traffic is None and "not used" in source
+    assert bench.profiled_traffic("map_install_stream", "no_such_workload") == (None, "not measured")
+    # a summary of the current source is used, one of another source is not
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    (tmp_path / "profiles").mkdir()
+    f = tmp_path / "profiles" / "k_w_traffic.md"
+    f.write_text(f"traffic_bytes_per_launch = 123\nkernel_source_sha16 = {now}\nmeasured = today\n")
+    assert bench.profiled_traffic("k", "w")[0] == 123
+    f.write_text("traffic_bytes_per_launch = 123\nkernel_source_sha16 = 0000000000000000\n")
+    assert bench.profiled_traffic("k", "w")[0] is None
     # every profile summary the design notes point to is committed
     design = (ROOT / "DESIGN.md").read_text()
     named = set(re.findall(r"profiles/([A-Za-z0-9_]+\.md)", design))
