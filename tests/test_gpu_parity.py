@@ -191,3 +191,30 @@ def test_out_of_range_slots_are_flagged_not_written():
                       block_table=h.block_table, page_size=16)
     flags = h.mapper.plan.read_errors()
     assert flags & 1
+
+
+@pytest.mark.parametrize("dim,dtype,support", [(64, torch.bfloat16, 3), (64, torch.float32, 2),
+                                               (128, torch.bfloat16, 3)])
+def test_support_maps_match_oracle(dim, dtype, support):
+    """Support-s maps at every kernel that takes them: the general kernel (D 64
+    bf16 and fp32 I/O) and the blocked support kernel (D 128 bf16, s = 3; a block
+    of 200 tokens is one full and one partial 128-token block)."""
+    print(f"support maps D={dim} {dtype} s={support}", flush=True)
+    g = torch.Generator().manual_seed(11 + dim + support)
+    ls, hs, lt, ht, n, p0 = 6, 2, 3, 2, 200, 300
+    layers = torch.stack([torch.randperm(ls, generator=g)[:support] for _ in range(lt * ht)])
+    spec = {"assign_layer": layers.view(lt, ht, support),
+            "assign_head": torch.randint(0, hs, (lt, ht, support), generator=g),
+            "k_weight": torch.randn(lt, ht, support * dim, dim, generator=g) / (support * dim) ** 0.5,
+            "v_weight": torch.randn(lt, ht, support * dim, dim, generator=g) / (support * dim) ** 0.5,
+            "k_bias": torch.randn(lt, ht, dim, generator=g) * 0.1,
+            "v_bias": torch.randn(lt, ht, dim, generator=g) * 0.1}
+    mapper = HeadwiseMapper.from_assignment(**spec, source_rope_theta=1e4, target_rope_theta=1e6, dtype=dtype,
+                                            device="cuda", max_positions=2048)
+    page = torch.randn(2, ls, n, hs, dim, generator=g).to(dtype)
+    out = mapper.map_page(page.cuda(), position_start=p0, output_device="cuda")
+    virtual = oi.virtual_source_page(page, spec["assign_layer"], spec["assign_head"])
+    ref = oi.assignment_mapper(spec, source_rope_theta=1e4, target_rope_theta=1e6).map_page(
+        virtual, position_start=p0)
+    bound = ot.magnitude_bound(page, spec, position_start=p0, source_theta=1e4, target_thetas=1e6)
+    print(ot.check_mapped(out, ref, bound, abs_factor=_factor(dtype)), flush=True)
