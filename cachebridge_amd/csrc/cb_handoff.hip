@@ -934,39 +934,54 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
 }
 
 // ---------------------------------------------------------------------------
-// Support kernel (support s > 1, head_dim 128, bf16 K/V): a blocked GEMM.
+// Support kernel (support s > 1, head_dim 128, bf16 K/V): a blocked GEMM with
+// producer and consumer waves.
 //
 // A target job's feature row is the concatenation of its s source rows, so
 // each job is a [T x s*128] . [s*128 x 128] contraction (the shipped top-8
-// recipe: 1024 input dims). A workgroup of 4 waves computes one 128-token
-// block of one job; two workgroups run on every CU. The input dims are
-// streamed in 2*s stages of 64 dims -- k-step pair {q, q + 2} (32 first-half
-// dims and their RoPE partners) of support member k, all members for q = 0
-// first -- through one LDS stage buffer:
-//   - W of the stage (8 row tiles x 2 k-steps x 2 terms, 32 KB) is loaded one
-//     stage ahead into registers;
-//   - the stage's input (128 tokens x 64 dims) is loaded two stages ahead and
-//     produced by the 256 threads, one token and 8 dims (+ partners) per
-//     task, two tasks each: keys are un-rotated and split into bf16 terms
-//     (the thread's un-rotation values of the current q stay in registers
-//     for s stages), values are written as loaded;
-//   - wave (h, c) multiplies row tiles {h*2 + q', +4} (an output half with
-//     its RoPE partners) by column tiles 4c .. 4c + 3 (64 tokens),
-//     accumulating across all stages in 64 VGPRs: each W fragment read from
-//     LDS feeds 4 column tiles and each input fragment 4 row tiles.
-// A stage is: multiply; barrier; write the next stage's W and input;
-// barrier. While one workgroup waits at a barrier or writes, the other keeps
-// the CU's MFMAs busy. Blocks are ordered job-major within each window class
-// and cut into one contiguous eighth per XCD, so an XCD's CUs run the blocks
-// of one job together and read its W (512 KB at s = 8) from their shared L2.
-// W is packed with the group output permutation (grp_out_dim); the epilogue
-// (bias as the first accumulator input, target RoPE, cast) stores whole
-// 64-byte chunks of the target rows.
+// recipe: 1024 input dims). An item is one 128-token block of one job. The
+// input dims of an item are streamed in 2*s stages of 64 dims -- k-step pair
+// {q, q + 2} (32 first-half dims and their RoPE partners) of support member
+// k, all members for q = 0 first.
+//
+// One persistent workgroup of 8 waves per CU. Waves 4..7 produce, waves
+// 0..3 consume, through a ring of two LDS stage buffers (W of the stage: 8
+// row tiles x 2 k-steps x 2 terms, 32 KB; the stage's input: 128 tokens x 64
+// dims x 2 terms, 32 KB):
+//   - a producer wave waits until the consumers have released the buffer,
+//     writes its quarter of the stage's W (loaded two stages ahead into
+//     registers) and of its input (loaded two stages ahead; keys un-rotated
+//     and split into bf16 terms, values written as loaded), signals the
+//     buffer full, and requests the loads of the stage after next, which may
+//     belong to the next item;
+//   - consumer wave (h, c) waits until all four producers have filled the
+//     buffer, multiplies row tiles {h*2 + q', +4} (an output half with its
+//     RoPE partners) by column tiles 4c .. 4c + 3 (64 tokens) into 64
+//     accumulator VGPRs, releases the buffer, and after an item's last stage
+//     runs the epilogue (bias as the first accumulator input, target RoPE,
+//     cast, stores of whole 64-byte chunks of the target rows).
+// Full and empty are monotonic per-buffer counters in LDS (a producer wave
+// adds 1 when its writes are done, a consumer wave adds 1 when its reads are
+// done), so no workgroup barrier is needed after start-up and the loads in
+// flight are never drained. LDS executes one wave's operations in order, so
+// data written before a counter update is visible to a wave that has seen the
+// update. Every wait is bounded: after about a second without progress a wave
+// flags the error word and sets a workgroup abort flag that ends every other
+// wait, so no launch can hang.
+//
+// Items: the jobs of each window class are dealt to the 8 XCDs round-robin
+// (job j of a class to XCD j % 8, keys and values alike), each XCD's items
+// are its jobs' blocks in order, and the workgroups of an XCD take every
+// (workgroups per XCD)-th item of that list. The workgroups of one XCD then
+// run the blocks of one job at a time and read its W (512 KB at s = 8) from
+// their shared L2, and every XCD gets the same mix of key and value jobs.
+// W is packed with the group output permutation (grp_out_dim).
 // ---------------------------------------------------------------------------
 
-constexpr int kSupTile = 128;                 // tokens per workgroup block
-constexpr int kSupWaves = 4;
+constexpr int kSupTile = 128;                 // tokens per item
+constexpr int kSupWaves = 8;                  // 4 consumer and 4 producer waves
 constexpr int kSupThreads = kSupWaves * kWave;
+constexpr int kSupRoleWaves = 4;
 
 // Output dim of row r (0..15) of row tile rt (0..7): tile rt = p*4 + h*2 + q
 // holds in lane group g = r / 4 the dims p*64 + h*32 + g*8 + q*4 + r % 4, so
@@ -977,128 +992,231 @@ __host__ __device__ inline int grp_out_dim(int rt, int r) {
   return (rt >> 2) * 64 + ((rt >> 1) & 1) * 32 + (r >> 2) * 8 + (rt & 1) * 4 + (r & 3);
 }
 
-// The stage buffer: W [row tile][k-step][term][lane] (32 KB) and the input
+// One stage buffer: W [row tile][k-step][term][lane] (32 KB) and the input
 // [column tile][k-step][term][lane] (32 KB).
 struct SupStage {
   uint4 w[8][2][2][kWave];
   uint4 x[8][2][2][kWave];
 };
 
-template <bool IS_K, bool SHARED, bool POS>
-__device__ void support_run(const MapArgs& a, SupStage& B, int32_t* trow, int32_t* tpos, float* bias,
-                            int job, int tok_lo, int tok_hi) {
-  // No implicit contraction: every fused multiply-add is written out.
-#pragma clang fp contract(off)
-  constexpr int D = 128, HALF = 64;
-  constexpr int kind = IS_K ? CB_KIND_K : CB_KIND_V;
-  constexpr int XT = IS_K ? 2 : 1;  // input terms (values are bf16-exact)
-  const int S = a.support;
-  const int nstage = 2 * S;
+struct SupShared {
+  SupStage ring[2];
+  int32_t trow[2][kSupTile];  // [item parity]: target row per token (-1: write nothing)
+  int32_t tpos[2][kSupTile];  // [item parity]: target position per token
+  float bias[2][128];         // [item parity]
+  uint32_t full[2];           // producer-wave fills of each buffer
+  uint32_t empty[2];          // consumer-wave releases of each buffer
+  uint32_t abort;             // set when a wait timed out
+};
 
+// The items of workgroup (x, y): see the header comment.
+struct SupItems {
+  int x, y, nwg;
+  int64_t next;  // position in XCD x's item list
+
+  struct Item {
+    int job, lo, hi;
+  };
+
+  __device__ bool get(const MapArgs& a, Item& it) const {
+    int64_t p = next;
+    for (int c = 0; c < a.ncls; ++c) {
+      const int nj = a.cls_unit_end[c] - a.cls_unit_begin[c];
+      const int mine = nj > x ? (nj - x + 7) / 8 : 0;
+      const int nch = a.cls_nchunks[c];
+      const int64_t count = static_cast<int64_t>(mine) * nch;
+      if (p < count) {
+        const int jl = static_cast<int>(p / nch), bk = static_cast<int>(p - static_cast<int64_t>(jl) * nch);
+        it.job = cload(a.unit_job + a.cls_unit_begin[c] + x + 8 * jl);
+        it.lo = a.cls_tok_first[c] + bk * kSupTile;
+        it.hi = min(it.lo + kSupTile, a.cls_tok_first[c] + a.cls_tok_count[c]);
+        return true;
+      }
+      p -= count;
+    }
+    return false;
+  }
+};
+
+__device__ inline CB_LDS uint32_t* lds_u32(uint32_t* p) { return (CB_LDS uint32_t*)p; }
+
+// Wait until *ctr >= target (or the workgroup aborted). Bounded: about 2^22
+// polls of at least 64 clocks each.
+__device__ inline void sup_wait(SupShared& S, uint32_t* ctr, uint32_t target, int* err) {
+  volatile CB_LDS uint32_t* c = lds_u32(ctr);
+  volatile CB_LDS uint32_t* ab = lds_u32(&S.abort);
+  for (int i = 0; i < (1 << 22); ++i) {
+    const uint32_t v = __builtin_amdgcn_readfirstlane(*c);
+    if (v >= target || __builtin_amdgcn_readfirstlane(*ab)) {
+      asm volatile("" ::: "memory");
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    atomicOr(err, 4);
+    *ab = 1;
+  }
+  asm volatile("" ::: "memory");
+}
+
+// Add 1 to *ctr once the wave's earlier LDS operations are done.
+__device__ inline void sup_signal(uint32_t* ctr) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if ((threadIdx.x & (kWave - 1)) == 0)
+    __hip_atomic_fetch_add(lds_u32(ctr), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Producer's view of an item: what its loads and its LDS side tables need.
+struct SupLoad {
+  bool valid, is_k;
+  int nstage;
+  gcptr wjob;           // the job's packed W, + lane * 16
+  const int32_t* pj;    // the job's support pairs
+  int kind;
+  int64_t soff[2];      // per task: source row byte offset, -1 for the zero row
+  int pos[2];           // per task: source position
+  const CB_GLOBAL float* ucos;
+  const CB_GLOBAL float* usin;
+};
+
+// Producer thread pt (0..255) of wave pw: tasks j = 0, 1 are column tile
+// 2 * pw + j, token 16 * (2 * pw + j) + (lane & 15), first-half dims
+// 16g + 8q .. +7 (g = lane >> 4) and their partners.
+__device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems::Item& it, int parity,
+                                  int pw, SupLoad& L) {
+  constexpr int D = 128;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane >> 4, col = lane & 15;
-  // Consumer: output half hh, column tiles 4cb .. 4cb + 3.
-  const int hh = wave >> 1, cb = wave & 1;
-
-  const int* jm = reinterpret_cast<const int*>(a.jobs + job);
-  const int mx = cload(jm), meta_y = cload(jm + 1);
-  const int sth = (meta_y >> 16) & 0xff, tth = (meta_y >> 24) & 0xff;
-  gptr tbase = const_cast<gptr>(layer_base(a.tgt, kind, mx & 0xffff)) +
-               static_cast<int64_t>((mx >> 16) - a.tgt.head_offset) * D * 2 + (hh * 32 + g * 8) * 2;
-  gptr sink = as_global(a.sink) + lane * 512;
-  gcptr zrow = as_global(a.zero);
-  const int32_t* pj = a.pairs + static_cast<size_t>(job) * S;
-  const CB_GLOBAL float* ucos = gtab(SHARED ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
-  const CB_GLOBAL float* usin = gtab(SHARED ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
-  const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
-  const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
-  gcptr wjob = as_global(a.w + static_cast<size_t>(job) * S * Gm<128, uint16_t>::W_U4) + lane * 16;
-
-  // Producer tasks j = 0, 1: column tile 2 * wave + j, token 16 * (2 * wave
-  // + j) + col, first-half dims 16g + 8q .. +7 and their partners. One row
-  // index serves every support member (they are layers of one source pool).
-  const int n = tok_hi - tok_lo;
-  int64_t soff[2];
-  int pos[2];
+  const int* jm = reinterpret_cast<const int*>(a.jobs + it.job);
+  const int meta_y = cload(jm + 1), meta_z = cload(jm + 2);
+  L.valid = true;
+  L.kind = meta_y & 0xff;
+  L.is_k = L.kind == CB_KIND_K;
+  L.nstage = 2 * a.support;
+  L.wjob = as_global(a.w + static_cast<size_t>(it.job) * a.support * Gm<128, uint16_t>::W_U4) + lane * 16;
+  L.pj = a.pairs + static_cast<size_t>(it.job) * a.support;
+  const int sth = (meta_y >> 16) & 0xff;
+  const bool shared = (meta_z & kJobSharedTables) != 0;
+  L.ucos = gtab(shared ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
+  L.usin = gtab(shared ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
+  const int n = it.hi - it.lo;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int pt = 16 * (2 * wave + j) + col;
-    const int tk = tok_lo + min(pt, n - 1);
+    const int pt = 16 * (2 * pw + j) + col;
+    const int tk = it.lo + min(pt, n - 1);
     const bool live = pt < n;
     const int64_t srow = row_of(a.src, tk);
     const int64_t drow = row_of(a.tgt, tk);
     const bool sok = srow >= 0 && srow < a.src.rows;
     const bool dok = drow >= 0 && drow < a.tgt.rows;
     if (live && !(sok && dok) && g == 0) atomicOr(a.err, (sok ? 0 : 1) | (dok ? 0 : 2));
-    soff[j] = live && sok ? srow * a.src.row_stride_b : -1;
-    pos[j] = position_of(a, tk);
+    L.soff[j] = live && sok ? srow * a.src.row_stride_b : -1;
+    L.pos[j] = position_of(a, tk);
     if (g == 0) {
-      // A token whose source row is out of range writes nothing (sink).
-      trow[pt] = live && sok && dok ? static_cast<int32_t>(drow) : -1;
-      tpos[pt] = pos[j];
+      // A token whose source row is out of range writes nothing.
+      S.trow[parity][pt] = live && sok && dok ? static_cast<int32_t>(drow) : -1;
+      S.tpos[parity][pt] = L.pos[j];
     }
   }
-  if (threadIdx.x < D) bias[threadIdx.x] = a.bias[static_cast<size_t>(job) * D + threadIdx.x];
+  const int pt = (threadIdx.x - kSupRoleWaves * kWave);
+  if (pt < D) S.bias[parity][pt] = a.bias[static_cast<size_t>(it.job) * D + pt];
+}
 
-  // Stage t: q = t / S, support member k = t % S, k-steps {q, q + 2}.
-  auto load_w = [&](int t, uint4 (&wv)[8]) {
-    const int q = t / S, k = t - q * S;
+// Loads of stage t of item L: W fragments (f = j * 4 + pw: row tile f >> 2,
+// k-step slot (f >> 1) & 1, term f & 1).
+__device__ inline void sup_issue_w(const MapArgs& a, const SupLoad& L, int t, int pw, uint4 (&w)[8]) {
+  const int S = a.support;
+  const int q = t >= S ? 1 : 0, k = t - q * S;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int f = j * kSupRoleWaves + pw;
+    const int rt = f >> 2, kk = (f >> 1) & 1, tm = f & 1;
+    const int ks = q + 2 * kk;
+    w[j] = gload<uint4>(L.wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
+  }
+}
+
+// Loads of stage t of item L: the two tasks' source dims and their partners.
+__device__ inline void sup_issue_x(const MapArgs& a, const SupLoad& L, int t, uint4 (&x)[2][2]) {
+  constexpr int HALF = 64;
+  const int S = a.support;
+  const int g = (threadIdx.x & (kWave - 1)) >> 4;
+  const int q = t >= S ? 1 : 0, k = t - q * S;
+  const int pr = cload(L.pj + k);
+  gcptr base = layer_base(a.src, L.kind, pr & 0xffff) + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * 128 * 2;
+  gcptr zrow = as_global(a.zero);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    gcptr p = (L.soff[j] >= 0 ? base + L.soff[j] : zrow) + (16 * g + 8 * q) * 2;
+    x[j][0] = gload<uint4>(p);
+    x[j][1] = gload<uint4>(p + HALF * 2);
+  }
+}
+
+// Un-rotation values of both tasks of item L for k-step pair q.
+__device__ inline void sup_issue_tab(const SupLoad& L, int q, float (&c)[2][8], float (&s)[2][8]) {
+  const int g = (threadIdx.x & (kWave - 1)) >> 4;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t off = tab_chunk<16>(L.pos[j], 2 * q + u, g);
+      const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(L.ucos + off);
+      const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(L.usin + off);
+      c[j][4 * u] = c4.x; c[j][4 * u + 1] = c4.y; c[j][4 * u + 2] = c4.z; c[j][4 * u + 3] = c4.w;
+      s[j][4 * u] = s4.x; s[j][4 * u + 1] = s4.y; s[j][4 * u + 2] = s4.z; s[j][4 * u + 3] = s4.w;
+    }
+}
+
+// Producer side of the whole launch (waves 4..7). Per stage n: wait for the
+// buffer, write W and the input (both loaded two stages ahead; the input
+// un-rotated with values loaded one stage ahead), signal, then request
+// the un-rotation values of stage n + 1 and W and the input of stage n + 2.
+// L is the item of the W and input loads; stage n + 1 always belongs to it
+// before it moves on.
+__device__ void sup_producer(const MapArgs& a, SupShared& S, SupItems items) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & (kWave - 1);
+  const int pw = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) - kSupRoleWaves;
+  const int Sup = a.support;
+  const int nstage = 2 * Sup;
+  SupItems::Item it;
+  if (!items.get(a, it)) return;
+  SupLoad L;
+  int load_parity = 0;
+  sup_decode(a, S, it, 0, pw, L);
+  uint4 wa[8], wb[8], xa[2][2], xb[2][2];
+  float tc[2][8], ts[2][8];
+  sup_issue_w(a, L, 0, pw, wa);
+  if (L.is_k) sup_issue_tab(L, 0, tc, ts);
+  sup_issue_x(a, L, 0, xa);
+  sup_issue_w(a, L, 1, pw, wb);
+  sup_issue_x(a, L, 1, xb);
+  int lt = 2;       // stage of L the next input loads are for
+  uint32_t n = 0;   // global stage index
+  bool p_is_k = L.is_k;
+
+  auto produce = [&](int t, uint4 (&w)[8], uint4 (&x)[2][2]) {
+    const int slot = n & 1;
+    sup_wait(S, &S.empty[slot], 4 * (n >> 1), a.err);
+    SupStage& B = S.ring[slot];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int f = j * kSupWaves + wave;  // (row tile, k-step slot, term)
-      const int rt = f >> 2, kk = (f >> 1) & 1, tm = f & 1;
-      const int ks = q + 2 * kk;
-      wv[j] = gload<uint4>(wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
+      const int f = j * kSupRoleWaves + pw;
+      B.w[f >> 2][(f >> 1) & 1][f & 1][lane] = w[j];
     }
-  };
-  auto store_w = [&](const uint4 (&wv)[8]) {
+    if (p_is_k) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int f = j * kSupWaves + wave;
-      B.w[f >> 2][(f >> 1) & 1][f & 1][lane] = wv[j];
-    }
-  };
-  auto load_x = [&](int t, uint4 (&xv)[2][2]) {
-    const int tc = min(t, nstage - 1);  // past the end: clamped, unused
-    const int q = tc / S, k = tc - q * S;
-    const int pr = cload(pj + k);
-    gcptr base = layer_base(a.src, kind, pr & 0xffff) + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * D * 2;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      gcptr p = (soff[j] >= 0 ? base + soff[j] : zrow) + (16 * g + 8 * q) * 2;
-      xv[j][0] = gload<uint4>(p);
-      xv[j][1] = gload<uint4>(p + HALF * 2);
-    }
-  };
-  // Un-rotation values of both tasks for k-step pair q: frequencies 16g + 8q + [0, 8).
-  float uc[2][8], us[2][8];
-  auto load_tab = [&](int q) {
-    if constexpr (IS_K) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int64_t off = tab_chunk<16>(pos[j], 2 * q + u, g);
-          const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(ucos + off);
-          const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(usin + off);
-          uc[j][4 * u] = c4.x; uc[j][4 * u + 1] = c4.y; uc[j][4 * u + 2] = c4.z; uc[j][4 * u + 3] = c4.w;
-          us[j][4 * u] = s4.x; us[j][4 * u + 1] = s4.y; us[j][4 * u + 2] = s4.z; us[j][4 * u + 3] = s4.w;
-        }
-    }
-  };
-  auto produce_x = [&](const uint4 (&xv)[2][2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int ct = 2 * wave + j;
-      if constexpr (IS_K) {
+      for (int j = 0; j < 2; ++j) {
+        const int ct = 2 * pw + j;
         float x1[8], x2[8];
-        unpack16<uint16_t>(xv[j][0], x1);
-        unpack16<uint16_t>(xv[j][1], x2);
+        unpack16<uint16_t>(x[j][0], x1);
+        unpack16<uint16_t>(x[j][1], x2);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float k1 = __builtin_fmaf(x1[e], uc[j][e], x2[e] * us[j][e]);
-          const float k2 = __builtin_fmaf(x2[e], uc[j][e], -(x1[e] * us[j][e]));
+          const float k1 = __builtin_fmaf(x1[e], tc[j][e], x2[e] * ts[j][e]);
+          const float k2 = __builtin_fmaf(x2[e], tc[j][e], -(x1[e] * ts[j][e]));
           x1[e] = k1;
           x2[e] = k2;
         }
@@ -1106,159 +1224,194 @@ __device__ void support_run(const MapArgs& a, SupStage& B, int32_t* trow, int32_
         split_terms<2, 8>(x1, t1);
         split_terms<2, 8>(x2, t2);
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          B.x[ct][0][x][lane] = make_uint4(t1[x][0], t1[x][1], t1[x][2], t1[x][3]);
-          B.x[ct][1][x][lane] = make_uint4(t2[x][0], t2[x][1], t2[x][2], t2[x][3]);
+        for (int v = 0; v < 2; ++v) {
+          B.x[ct][0][v][lane] = make_uint4(t1[v][0], t1[v][1], t1[v][2], t1[v][3]);
+          B.x[ct][1][v][lane] = make_uint4(t2[v][0], t2[v][1], t2[v][2], t2[v][3]);
         }
-      } else {
-        B.x[ct][0][0][lane] = xv[j][0];
-        B.x[ct][1][0][lane] = xv[j][1];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ct = 2 * pw + j;
+        B.x[ct][0][0][lane] = x[j][0];
+        B.x[ct][1][0][lane] = x[j][1];
       }
     }
+    sup_signal(&S.full[slot]);
+    ++n;
+    if (!L.valid) return;
+    // Stage n (the next one) is stage lt - 1 of L.
+    const int tn = lt - 1;
+    if (tn < nstage && L.is_k && (tn == 0 || tn == Sup)) sup_issue_tab(L, tn == 0 ? 0 : 1, tc, ts);
+    if (lt == nstage) {
+      items.next += items.nwg;
+      if (!items.get(a, it)) {
+        L.valid = false;
+        return;
+      }
+      load_parity ^= 1;
+      sup_decode(a, S, it, load_parity, pw, L);
+      lt = 0;
+    }
+    sup_issue_w(a, L, lt, pw, w);
+    sup_issue_x(a, L, lt, x);
+    ++lt;
+    (void)t;
   };
 
-  f32x4 acc[4][4];  // [row tile p*2 + q'][column tile]
-  auto multiply = [&](bool first) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      bf16x8 xv[4][XT];
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int x = 0; x < XT; ++x) xv[c][x] = __builtin_bit_cast(bf16x8, B.x[4 * cb + c][kk][x][lane]);
-      bf16x8 wv[4][2];
-#pragma unroll
-      for (int rl = 0; rl < 4; ++rl) {
-        const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
-#pragma unroll
-        for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, B.w[rt][kk][tm][lane]);
-      }
-      int pi = 0;
-      for_products<XT, 2>([&](int ii, int jj) {
-#pragma unroll
-        for (int rl = 0; rl < 4; ++rl)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            f32x4 cin;
-            if (first && kk == 0 && pi == 0) {
-              const float* bp = bias + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
-              cin = f32x4{bp[0], bp[1], bp[2], bp[3]};
-            } else {
-              cin = acc[rl][c];
-            }
-            acc[rl][c] = mfma(wv[rl][jj], xv[c][ii], cin);
-          }
-        ++pi;
-      });
+  SupItems prod = items;  // the producing item (behind L by at most one)
+  for (;;) {
+    for (int t = 0; t < nstage; t += 2) {
+      produce(t, wa, xa);
+      produce(t + 1, wb, xb);
     }
-  };
-
-  // Prologue: stage 0 written; stage 1's W and input requested.
-  uint4 wn[8], xa[2][2], xb[2][2];
-  load_w(0, wn);
-  load_x(0, xa);
-  load_x(1, xb);
-  load_tab(0);
-  __syncthreads();  // trow, tpos and bias written (and a previous block's LDS reads done)
-  store_w(wn);
-  produce_x(xa);
-  // Barriers inside the stage loop fence LDS only, so the loads issued for
-  // later stages stay in flight (a full barrier would wait for them).
-  auto lds_barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
-  load_w(1, wn);
-  load_x(2, xa);
-  lds_barrier();
-  // Stage t multiplies; then the buffer is rewritten with stage t+1 (W from
-  // wn, input from the set loaded two stages earlier) while stage t+2's W
-  // and stage t+3's input are requested. xb / xa alternate as the input of
-  // the next stage.
-  auto stage = [&](int t, uint4 (&x_next)[2][2]) {
-    multiply(t == 0);
-    __builtin_amdgcn_sched_barrier(0);
-    lds_barrier();  // every wave has read stage t
-    if (t + 1 < nstage) {
-      if (t + 1 == S) load_tab(1);  // the second k-step pair starts
-      store_w(wn);
-      produce_x(x_next);
-      if (t + 2 < nstage) load_w(t + 2, wn);
-      load_x(t + 3, x_next);  // this set was just consumed; it becomes stage t+3's input
-      lds_barrier();
-    }
-  };
-  for (int t = 0; t < nstage; t += 2) {
-    stage(t, xb);
-    stage(t + 1, xa);
-  }
-
-  // Epilogue: target RoPE, cast, store.
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int tok = (4 * cb + c) * 16 + col;
-    const int row = trow[tok];
-    float y1[8], y2[8];
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        y1[4 * q + i] = acc[q][c][i];
-        y2[4 * q + i] = acc[2 + q][c][i];
-      }
-    if constexpr (IS_K) {
-      const int tp = tpos[tok];
-      float cv[8], sv[8];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int64_t off = tab_chunk<16>(tp, 2 * (g & 1) + u, 2 * hh + (g >> 1));
-        const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
-        const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
-        cv[4 * u] = c4.x; cv[4 * u + 1] = c4.y; cv[4 * u + 2] = c4.z; cv[4 * u + 3] = c4.w;
-        sv[4 * u] = s4.x; sv[4 * u + 1] = s4.y; sv[4 * u + 2] = s4.z; sv[4 * u + 3] = s4.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a1 = y1[e], a2 = y2[e];
-        y1[e] = __builtin_fmaf(a1, cv[e], -(a2 * sv[e]));
-        y2[e] = __builtin_fmaf(a2, cv[e], a1 * sv[e]);
-      }
-    }
-    uint32_t o1[4], o2[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o1[i] = pack_bf16(y1[2 * i], y1[2 * i + 1]);
-      o2[i] = pack_bf16(y2[2 * i], y2[2 * i + 1]);
-    }
-    gptr dst = row >= 0 ? tbase + static_cast<int64_t>(row) * a.tgt.row_stride_b : sink;
-    gstore<uint4>(dst, make_uint4(o1[0], o1[1], o1[2], o1[3]));
-    gstore<uint4>(dst + HALF * 2, make_uint4(o2[0], o2[1], o2[2], o2[3]));
+    prod.next += prod.nwg;
+    SupItems::Item pit;
+    if (!prod.get(a, pit)) break;
+    const int* jm = reinterpret_cast<const int*>(a.jobs + pit.job);
+    p_is_k = (cload(jm + 1) & 0xff) == CB_KIND_K;
   }
 }
 
-template <bool POS>
-__global__ __launch_bounds__(kSupThreads, 2) void map_install_support_kernel(MapArgs a) {
-  __shared__ SupStage B;
-  __shared__ int32_t trow[kSupTile];
-  __shared__ int32_t tpos[kSupTile];
-  __shared__ float bias[128];
-  // Item L of XCD b & 7's contiguous eighth: window class, then job, then
-  // 128-token block, so an XCD's CUs run the blocks of one job together.
-  const int per = a.padded_items >> 3;
-  const int L = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-  if (L >= a.total_items) return;
-  int c = 0;
-  while (c + 1 < a.ncls && L >= a.cls_item_begin[c + 1]) ++c;
-  const int lc = L - a.cls_item_begin[c];
-  const int nch = a.cls_nchunks[c];
-  const int job = __builtin_amdgcn_readfirstlane(cload(a.unit_job + a.cls_unit_begin[c] + lc / nch));
-  const int lo = a.cls_tok_first[c] + (lc % nch) * kSupTile;
-  const int hi = min(lo + kSupTile, a.cls_tok_first[c] + a.cls_tok_count[c]);
-  const int* mp = reinterpret_cast<const int*>(a.jobs + job);
-  const int meta_y = cload(mp + 1), meta_z = cload(mp + 2);
-  if ((meta_y & 0xff) == CB_KIND_K) {
-    if (meta_z & kJobSharedTables) support_run<true, true, POS>(a, B, trow, tpos, bias, job, lo, hi);
-    else support_run<true, false, POS>(a, B, trow, tpos, bias, job, lo, hi);
-  } else {
-    support_run<false, false, POS>(a, B, trow, tpos, bias, job, lo, hi);
+// Consumer side of the whole launch (waves 0..3).
+__device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
+#pragma clang fp contract(off)
+  constexpr int D = 128, HALF = 64;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g = lane >> 4, col = lane & 15;
+  const int hh = wave >> 1, cb = wave & 1;
+  const int Sup = a.support;
+  const int nstage = 2 * Sup;
+  gptr sink = as_global(a.sink) + lane * 512;
+  uint32_t n = 0;
+  int parity = 0;
+  SupItems::Item it;
+  for (; items.get(a, it); items.next += items.nwg, parity ^= 1) {
+    const int* jm = reinterpret_cast<const int*>(a.jobs + it.job);
+    const int mx = cload(jm), meta_y = cload(jm + 1);
+    const int kind = meta_y & 0xff;
+    const int tth = (meta_y >> 24) & 0xff;
+    gptr tbase = const_cast<gptr>(layer_base(a.tgt, kind, mx & 0xffff)) +
+                 static_cast<int64_t>((mx >> 16) - a.tgt.head_offset) * D * 2 + (hh * 32 + g * 8) * 2;
+    const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
+    const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
+
+    auto run = [&](auto is_k_tag) {
+      constexpr bool IS_K = decltype(is_k_tag)::value;
+      constexpr int XT = IS_K ? 2 : 1;
+      f32x4 acc[4][4];  // [row tile p*2 + q'][column tile]
+      float4 ec[4][2], es[4][2];  // epilogue rotation values, requested two stages ahead
+      for (int t = 0; t < nstage; ++t) {
+        const int slot = n & 1;
+        sup_wait(S, &S.full[slot], 4 * ((n >> 1) + 1), a.err);
+        if constexpr (IS_K) {
+          if (t == nstage - 2) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const int tp = S.tpos[parity][(4 * cb + c) * 16 + col];
+#pragma unroll
+              for (int u = 0; u < 2; ++u) {
+                const int64_t off = tab_chunk<16>(tp, 2 * (g & 1) + u, 2 * hh + (g >> 1));
+                ec[c][u] = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
+                es[c][u] = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
+              }
+            }
+          }
+        }
+        const SupStage& B = S.ring[slot];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          bf16x8 xv[4][XT];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int x = 0; x < XT; ++x) xv[c][x] = __builtin_bit_cast(bf16x8, B.x[4 * cb + c][kk][x][lane]);
+          bf16x8 wv[4][2];
+#pragma unroll
+          for (int rl = 0; rl < 4; ++rl) {
+            const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, B.w[rt][kk][tm][lane]);
+          }
+          int pi = 0;
+          for_products<XT, 2>([&](int ii, int jj) {
+#pragma unroll
+            for (int rl = 0; rl < 4; ++rl)
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                f32x4 cin;
+                if (t == 0 && kk == 0 && pi == 0) {
+                  const float* bp = S.bias[parity] + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
+                  cin = f32x4{bp[0], bp[1], bp[2], bp[3]};
+                } else {
+                  cin = acc[rl][c];
+                }
+                acc[rl][c] = mfma(wv[rl][jj], xv[c][ii], cin);
+              }
+            ++pi;
+          });
+        }
+        asm volatile("" ::: "memory");
+        sup_signal(&S.empty[slot]);
+        ++n;
+      }
+      // Epilogue: target RoPE, cast, store.
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int tok = (4 * cb + c) * 16 + col;
+        const int row = S.trow[parity][tok];
+        float y1[8], y2[8];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            y1[4 * q + i] = acc[q][c][i];
+            y2[4 * q + i] = acc[2 + q][c][i];
+          }
+        if constexpr (IS_K) {
+          const float cv[8] = {ec[c][0].x, ec[c][0].y, ec[c][0].z, ec[c][0].w,
+                               ec[c][1].x, ec[c][1].y, ec[c][1].z, ec[c][1].w};
+          const float sv[8] = {es[c][0].x, es[c][0].y, es[c][0].z, es[c][0].w,
+                               es[c][1].x, es[c][1].y, es[c][1].z, es[c][1].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float a1 = y1[e], a2 = y2[e];
+            y1[e] = __builtin_fmaf(a1, cv[e], -(a2 * sv[e]));
+            y2[e] = __builtin_fmaf(a2, cv[e], a1 * sv[e]);
+          }
+        }
+        uint32_t o1[4], o2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o1[i] = pack_bf16(y1[2 * i], y1[2 * i + 1]);
+          o2[i] = pack_bf16(y2[2 * i], y2[2 * i + 1]);
+        }
+        gptr dst = row >= 0 ? tbase + static_cast<int64_t>(row) * a.tgt.row_stride_b : sink;
+        gstore<uint4>(dst, make_uint4(o1[0], o1[1], o1[2], o1[3]));
+        gstore<uint4>(dst + HALF * 2, make_uint4(o2[0], o2[1], o2[2], o2[3]));
+      }
+    };
+    if (kind == CB_KIND_K) run(std::integral_constant<bool, true>{});
+    else run(std::integral_constant<bool, false>{});
   }
+}
+
+__global__ __launch_bounds__(kSupThreads, 1) void map_install_support_kernel(MapArgs a) {
+  __shared__ SupShared S;
+  if (threadIdx.x == 0) {
+    S.full[0] = S.full[1] = 0;
+    S.empty[0] = S.empty[1] = 0;
+    S.abort = 0;
+  }
+  __syncthreads();
+  SupItems items;
+  items.x = blockIdx.x & 7;
+  items.nwg = gridDim.x >> 3;
+  items.y = blockIdx.x >> 3;
+  items.next = items.y;
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) < kSupRoleWaves) sup_consumer(a, S, items);
+  else sup_producer(a, S, items);
 }
 
 // ---------------------------------------------------------------------------
@@ -2229,6 +2382,8 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
   int chunk = tokens_per_workgroup > 0 ? tokens_per_workgroup : default_tokens;
   if (tokens_per_workgroup < 0 || chunk < unit || chunk % unit)
     return fail(CB_EINVAL, "tokens_per_workgroup must be a positive multiple of %d", unit);
+  // The support kernel's items are fixed 128-token blocks; the knob does not apply.
+  if (p->support_gemm) chunk = kSupTile;
   a.w = static_cast<const uint4*>(p->d_w);
   a.bias = p->d_bias;
   a.jobs = p->d_jobs;
@@ -2254,6 +2409,7 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
     if (first[c] + count[c] > INT32_MAX) return fail(CB_EINVAL, "launch too large");
     const int64_t nch = (count[c] + chunk - 1) / chunk;
     a.cls_unit_begin[c] = p->cls_unit_begin[c];
+    a.cls_unit_end[c] = p->cls_unit_end[c];
     a.cls_tok_first[c] = static_cast<int32_t>(first[c]);
     a.cls_tok_count[c] = static_cast<int32_t>(count[c]);
     a.cls_nchunks[c] = static_cast<int32_t>(std::max<int64_t>(nch, 1));
@@ -2312,9 +2468,9 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
       else hipLaunchKernelGGL((map_install_stream_kernel<64, float, false>), grid, block, 0, s, a);
     }
   } else if (p->support_gemm) {
-    static_assert(kGenSubTokens == kSupTile, "one 128-token block per item");
-    if (a.pos) hipLaunchKernelGGL((map_install_support_kernel<true>), grid, dim3(kSupThreads), 0, s, a);
-    else hipLaunchKernelGGL((map_install_support_kernel<false>), grid, dim3(kSupThreads), 0, s, a);
+    // One persistent workgroup per CU; 8 per XCD at least.
+    const unsigned per_xcd = static_cast<unsigned>(std::max(1, p->num_cus / 8));
+    hipLaunchKernelGGL(map_install_support_kernel, dim3(8 * per_xcd), dim3(kSupThreads), 0, s, a);
   } else {
     if (D == 128 && p->ntw == 2)
       hipLaunchKernelGGL((map_install_gen_kernel<128, uint16_t>), grid, block, 0, s, a);

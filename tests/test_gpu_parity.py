@@ -218,3 +218,26 @@ def test_support_maps_match_oracle(dim, dtype, support):
         virtual, position_start=p0)
     bound = ot.magnitude_bound(page, spec, position_start=p0, source_theta=1e4, target_thetas=1e6)
     print(ot.check_mapped(out, ref, bound, abs_factor=_factor(dtype)), flush=True)
+
+
+def test_support_items_ignore_tokens_per_workgroup():
+    """The support kernel's items are fixed 128-token blocks: a launch with a
+    larger tokens_per_workgroup writes every token, bit-identically."""
+    print("support s8 tokens_per_workgroup", flush=True)
+    sh = synthetic.shape("tp4_s8", tokens=600)
+    sh.target_layers = 4
+    h = synthetic.make_handoff(sh, target_pages=64)
+    bufs = h.target_pool.k_buffer + h.target_pool.v_buffer
+    for b in bufs:
+        b.zero_()
+    h.run()
+    torch.cuda.synchronize()
+    first = [b.clone() for b in bufs]
+    for b in bufs:
+        b.zero_()
+    h.run(tokens_per_workgroup=512)
+    torch.cuda.synchronize()
+    assert h.mapper.plan.read_errors() == 0
+    for a_, b_ in zip(first, bufs):
+        assert torch.equal(a_, b_)
+    assert all(bool(b.abs().sum() > 0) for b in first)
