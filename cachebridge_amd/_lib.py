@@ -23,6 +23,7 @@ CB_EHIP = -5
 CB_DTYPE_BF16 = 0
 CB_DTYPE_F32 = 1
 CB_DTYPE_F64 = 2
+CB_DTYPE_F16 = 3
 CB_KIND_K = 0
 CB_KIND_V = 1
 CB_INDEX_IDENTITY = 0

@@ -1645,6 +1645,189 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
   }
 }
 
+// ---------------------------------------------------------------------------
+// Generic kernel: any even head_dim up to 512, any support, bf16 / fp16 /
+// fp32 K/V, computed in fp32 with FMAs (no split terms, no MFMA). It serves
+// the shapes and dtypes the MFMA kernels do not take; the configured
+// workloads never reach it.
+//
+// One workgroup of 256 threads per item (one job, a token range), 32-token
+// tiles. Per tile and support member k, the tile's source rows are gathered,
+// keys un-rotated (dims p and p + D/2 of a thread's pairs together), and the
+// fp32 values staged in LDS; each thread owns one output dim pair p, p + D/2
+// (threads_per_pair = 256 / (D/2) threads share a pair and split the
+// tokens) and accumulates sum_i x[t][i] * W[k*D + i][p] over the member's D
+// input dims. After the last member: + bias (the reference adds it after
+// the product), target RoPE on the pair, cast (round to nearest even),
+// store. Plan data for this kernel: W as fp32 [job][s*D][D] and the RoPE
+// tables in natural [theta][position][D/2] order.
+// ---------------------------------------------------------------------------
+
+constexpr int kAnyThreads = 256;
+constexpr int kAnyTile = 32;        // tokens per tile
+constexpr int kAnyMaxDim = 512;
+constexpr int kAnyMaxTok = kAnyTile;  // tokens per thread at most (one thread per pair)
+
+template <typename IO>
+struct AnyIO;
+template <>
+struct AnyIO<uint16_t> {  // bf16
+  static __device__ float get(const CB_GLOBAL uint16_t* p) { return bf2f(*p); }
+  static __device__ void put(CB_GLOBAL uint16_t* p, float v) { *p = f2bf(v); }
+};
+template <>
+struct AnyIO<_Float16> {
+  static __device__ float get(const CB_GLOBAL _Float16* p) { return static_cast<float>(*p); }
+  static __device__ void put(CB_GLOBAL _Float16* p, float v) { *p = static_cast<_Float16>(v); }
+};
+template <>
+struct AnyIO<float> {
+  static __device__ float get(const CB_GLOBAL float* p) { return *p; }
+  static __device__ void put(CB_GLOBAL float* p, float v) { *p = v; }
+};
+
+template <typename IO>
+__global__ __launch_bounds__(kAnyThreads) void map_install_any_kernel(MapArgs a, int D) {
+#pragma clang fp contract(off)
+  __shared__ float xs[kAnyTile][kAnyMaxDim];
+  __shared__ int64_t trow[kAnyTile];
+  __shared__ int64_t srow[kAnyTile];  // source row, -1: zero source values
+  __shared__ int32_t tpos[kAnyTile];
+  Work wk;
+  if (!decode_work(a, &wk)) return;
+  const int S = a.support;
+  const int half = D / 2;
+  const int job = wk.job;
+  const int* jm = reinterpret_cast<const int*>(a.jobs + job);
+  const int mx = cload(jm), meta_y = cload(jm + 1);
+  const int kind = meta_y & 0xff;
+  const bool is_k = kind == CB_KIND_K;
+  const int sth = (meta_y >> 16) & 0xff, tth = (meta_y >> 24) & 0xff;
+  const int64_t eb = sizeof(IO);
+  // Un-rotation tables cos/m, sin/m and rotation tables, natural order.
+  const CB_GLOBAL float* ucos = gtab(a.ucos_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* usin = gtab(a.usin_tab) + sth * a.theta_stride;
+  const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
+  const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
+  gptr tbase = const_cast<gptr>(layer_base(a.tgt, kind, mx & 0xffff)) +
+               static_cast<int64_t>((mx >> 16) - a.tgt.head_offset) * D * eb;
+  const CB_GLOBAL float* W = gtab(reinterpret_cast<const float*>(a.w)) + static_cast<int64_t>(job) * S * D * D;
+  const CB_GLOBAL float* bias = gtab(a.bias) + static_cast<int64_t>(job) * D;
+  // This thread's dim pair and tokens.
+  const int tpp = max(1, kAnyThreads / half);       // threads per pair
+  const int p = threadIdx.x / tpp, sub = threadIdx.x % tpp;
+  const bool active = p < half;
+  const int toks = (kAnyTile + tpp - 1) / tpp;      // tokens per thread
+  int errbits = 0;
+
+  for (int lo = wk.tok_lo; lo < wk.tok_hi; lo += kAnyTile) {
+    const int n = min(kAnyTile, wk.tok_hi - lo);
+    __syncthreads();  // the previous tile's LDS reads are done
+    if (threadIdx.x < kAnyTile) {
+      const int t = threadIdx.x;
+      const int tk = lo + min(t, n - 1);
+      const int64_t s = row_of(a.src, tk), d = row_of(a.tgt, tk);
+      const bool live = t < n;
+      const bool sok = s >= 0 && s < a.src.rows, dok = d >= 0 && d < a.tgt.rows;
+      if (live) errbits |= (sok ? 0 : 1) | (dok ? 0 : 2);
+      // A token whose source row is out of range writes nothing.
+      trow[t] = live && sok && dok ? d : -1;
+      srow[t] = live && sok ? s : -1;
+      tpos[t] = position_of(a, tk);
+    }
+    float acc[kAnyMaxTok][2];
+#pragma unroll
+    for (int m = 0; m < kAnyMaxTok; ++m) acc[m][0] = acc[m][1] = 0.f;
+    for (int k = 0; k < S; ++k) {
+      __syncthreads();  // rows ready / previous member's reads done
+      const int pr = cload(a.pairs + static_cast<size_t>(job) * S + k);
+      gcptr sbase = layer_base(a.src, kind, pr & 0xffff) + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * D * eb;
+      for (int e = threadIdx.x; e < kAnyTile * half; e += kAnyThreads) {
+        const int t = e / half, j = e % half;
+        const int pos = tpos[t];
+        const int64_t s = srow[t];
+        float x1 = 0.f, x2 = 0.f;
+        if (s >= 0) {
+          const CB_GLOBAL IO* row = reinterpret_cast<const CB_GLOBAL IO*>(sbase + s * a.src.row_stride_b);
+          x1 = AnyIO<IO>::get(row + j);
+          x2 = AnyIO<IO>::get(row + j + half);
+        }
+        if (is_k) {
+          const float c = ucos[static_cast<int64_t>(pos) * half + j];
+          const float sn = usin[static_cast<int64_t>(pos) * half + j];
+          const float k1 = __builtin_fmaf(x1, c, x2 * sn);
+          const float k2 = __builtin_fmaf(x2, c, -(x1 * sn));
+          x1 = k1;
+          x2 = k2;
+        }
+        xs[t][j] = x1;
+        xs[t][j + half] = x2;
+      }
+      __syncthreads();
+      if (active) {
+        const CB_GLOBAL float* wk_ = W + static_cast<int64_t>(k) * D * D;
+        for (int i = 0; i < D; ++i) {
+          const float w1 = wk_[static_cast<int64_t>(i) * D + p];
+          const float w2 = wk_[static_cast<int64_t>(i) * D + p + half];
+#pragma unroll
+          for (int m = 0; m < kAnyMaxTok; ++m) {
+            if (m < toks) {
+              const int t = sub + m * tpp;
+              if (t < kAnyTile) {
+                const float x = xs[t][i];
+                acc[m][0] = __builtin_fmaf(x, w1, acc[m][0]);
+                acc[m][1] = __builtin_fmaf(x, w2, acc[m][1]);
+              }
+            }
+          }
+        }
+      }
+    }
+    if (active) {
+      const float b1 = bias[p], b2 = bias[p + half];
+#pragma unroll
+      for (int m = 0; m < kAnyMaxTok; ++m) {
+        if (m >= toks) continue;
+        const int t = sub + m * tpp;
+        if (t >= n) continue;
+        const int64_t row = trow[t];
+        if (row < 0) continue;
+        float y1 = acc[m][0] + b1, y2 = acc[m][1] + b2;
+        if (is_k) {
+          const int pos = tpos[t];
+          const float c = rcos[static_cast<int64_t>(pos) * half + p];
+          const float sn = rsin[static_cast<int64_t>(pos) * half + p];
+          const float r1 = __builtin_fmaf(y1, c, -(y2 * sn));
+          const float r2 = __builtin_fmaf(y2, c, y1 * sn);
+          y1 = r1;
+          y2 = r2;
+        }
+        CB_GLOBAL IO* out = reinterpret_cast<CB_GLOBAL IO*>(tbase + row * a.tgt.row_stride_b);
+        AnyIO<IO>::put(out + p, y1);
+        AnyIO<IO>::put(out + p + half, y2);
+      }
+    }
+  }
+  if (errbits) atomicOr(a.err, errbits);
+}
+
+// Plan data of the generic kernel: W [job][s*D][D] and bias [job][D] copied
+// in sorted job order.
+__global__ void copy_weights_kernel(const float* __restrict__ w, const float* __restrict__ bias,
+                                    const int32_t* __restrict__ order, int njobs, int per_job_w, int D,
+                                    float* __restrict__ wp, float* __restrict__ bp) {
+  const int64_t total = static_cast<int64_t>(njobs) * per_job_w;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t j = idx / per_job_w;
+    wp[idx] = w[static_cast<int64_t>(order[j]) * per_job_w + idx % per_job_w];
+  }
+  const int64_t nb = static_cast<int64_t>(njobs) * D;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < nb;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    bp[idx] = bias[static_cast<int64_t>(order[idx / D]) * D + idx % D];
+}
+
 // Plan tables from standard [theta][pos][D/2] cos/sin: rotation tables and
 // un-rotation tables cos/m, sin/m (m = max(cos^2 + sin^2, FLT_MIN)), both in
 // the permuted half-row layout; also max |m - 1| per theta set (as float bits).
@@ -1653,7 +1836,7 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
 __global__ __launch_bounds__(256) void prepare_tables_kernel(
     const float* __restrict__ c, const float* __restrict__ s, float* __restrict__ rc,
     float* __restrict__ rs, float* __restrict__ uc, float* __restrict__ us, int half,
-    int64_t per_theta, int64_t out_per_theta, unsigned* __restrict__ norm_dev) {
+    int64_t per_theta, int64_t out_per_theta, unsigned* __restrict__ norm_dev, int natural) {
 #pragma clang fp contract(off)
   __shared__ unsigned red[256];
   const int64_t base = static_cast<int64_t>(blockIdx.y) * per_theta;
@@ -1663,7 +1846,8 @@ __global__ __launch_bounds__(256) void prepare_tables_kernel(
     const int64_t i = base + k;
     const float cc = c[i], ss = s[i];
     const float m = fmaxf(cc * cc + ss * ss, 1.17549435e-38f);
-    const int64_t o = blockIdx.y * out_per_theta + tab_offset(half, k / half, static_cast<int>(k % half));
+    const int64_t o = blockIdx.y * out_per_theta +
+                      (natural ? k : tab_offset(half, k / half, static_cast<int>(k % half)));
     rc[o] = cc;
     rs[o] = ss;
     uc[o] = cc / m;
@@ -1999,6 +2183,7 @@ struct cb_plan {
   int ntw = 2;
   int elem_bytes = 2;
   bool support_gemm = false;  // support > 1, head_dim 128, bf16: map_install_support_kernel
+  bool generic = false;       // map_install_any_kernel: shapes / dtypes the MFMA kernels do not take
   int num_windows = 1;
   int window_size[kMaxClasses] = {0, 0, 0, 0};
   int cls_unit_begin[kMaxClasses] = {0, 0, 0, 0};
@@ -2050,7 +2235,9 @@ int upload(Tp** dst, const void* src, size_t bytes, int64_t* total) {
   return CB_OK;
 }
 
-int to_dev_rows(const cb_rows& r, int elem_bytes, DevRows* out) {
+// align: the byte alignment the launch needs of strides and bases (16 for the
+// vector kernels, one element for the generic kernel).
+int to_dev_rows(const cb_rows& r, int elem_bytes, DevRows* out, int align = 16) {
   out->k_layers = r.k_layers;
   out->v_layers = r.v_layers;
   out->k_base = static_cast<const char*>(r.k_base);
@@ -2076,10 +2263,10 @@ int to_dev_rows(const cb_rows& r, int elem_bytes, DevRows* out) {
   if (!r.k_layers && (!r.k_base || !r.v_base))
     return fail(CB_EINVAL, "either per-layer pointer arrays or k_base/v_base are required");
   if (r.k_layers && !r.v_layers) return fail(CB_EINVAL, "v_layers required with k_layers");
-  if ((out->row_stride_b % 16) || (out->layer_stride_b % 16))
-    return fail(CB_EINVAL, "row and layer strides must be multiples of 16 bytes");
-  if ((reinterpret_cast<uintptr_t>(r.k_base) | reinterpret_cast<uintptr_t>(r.v_base)) % 16)
-    return fail(CB_EINVAL, "k_base/v_base must be 16-byte aligned");
+  if ((out->row_stride_b % align) || (out->layer_stride_b % align))
+    return fail(CB_EINVAL, "row and layer strides must be multiples of %d bytes", align);
+  if ((reinterpret_cast<uintptr_t>(r.k_base) | reinterpret_cast<uintptr_t>(r.v_base)) % align)
+    return fail(CB_EINVAL, "k_base/v_base must be %d-byte aligned", align);
   return CB_OK;
 }
 
@@ -2096,8 +2283,10 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   int64_t bytes = 0;
   CB_HIP(hipGetDevice(&p->device));
   p->ntw = d->io_dtype == CB_DTYPE_BF16 ? 2 : 3;
-  p->elem_bytes = d->io_dtype == CB_DTYPE_BF16 ? 2 : 4;
-  p->support_gemm = S > 1 && D == 128 && p->ntw == 2;
+  p->elem_bytes = d->io_dtype == CB_DTYPE_F32 ? 4 : 2;
+  p->generic = !((d->io_dtype == CB_DTYPE_BF16 && (D == 64 || D == 128)) ||
+                 (d->io_dtype == CB_DTYPE_F32 && D == 64));
+  p->support_gemm = !p->generic && S > 1 && D == 128 && p->ntw == 2;
   p->num_windows = d->num_windows;
   for (int c = 0; c < kMaxClasses; ++c) {
     p->window_size[c] = c < d->num_windows ? d->window_size[c] : 0;
@@ -2114,7 +2303,7 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   p->max_tgt_head = 0;
   // Units: runs of up to kUnitJobs consecutive jobs of one group for the
   // streaming kernel (s == 1); single jobs for the general kernel.
-  const int unit_cap = S == 1 ? kUnitJobs : 1;
+  const int unit_cap = S == 1 && !p->generic ? kUnitJobs : 1;
   for (int i = 0; i < nj; ++i) {
     const int j = order[i];
     jobs[i] = make_int4(d->job_target_layer[j] | (d->job_target_head[j] << 16),
@@ -2157,7 +2346,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     p->num_cus = std::max(8, std::min(cus, kMaxStreamBlocks) / 8 * 8);
   }
 
-  const size_t w_elems = static_cast<size_t>(nj) * S * (D / 16) * (D / 32) * p->ntw * kWave * 8;
+  const size_t w_bytes = p->generic ? static_cast<size_t>(nj) * S * D * D * 4
+                                    : static_cast<size_t>(nj) * S * (D / 16) * (D / 32) * p->ntw * kWave * 8 * 2;
   const int64_t padded_positions = (static_cast<int64_t>(d->table_positions) + kTabBlock - 1) / kTabBlock * kTabBlock;
   const size_t table = static_cast<size_t>(d->num_thetas) * padded_positions * (D / 2);
   int rc;
@@ -2167,7 +2357,7 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   if ((rc = upload(&p->d_unit_group, unit_group.data(), unit_group.size() * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_group_unit_start, group_unit_start.data(), group_unit_start.size() * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_group_unit_count, group_unit_count.data(), group_unit_count.size() * 4, &bytes))) return rc;
-  if ((rc = upload(&p->d_w, nullptr, w_elems * 2, &bytes))) return rc;
+  if ((rc = upload(&p->d_w, nullptr, w_bytes, &bytes))) return rc;
   if ((rc = upload(&p->d_bias, nullptr, static_cast<size_t>(nj) * D * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_cos, nullptr, table * 4, &bytes))) return rc;
   if ((rc = upload(&p->d_sin, nullptr, table * 4, &bytes))) return rc;
@@ -2187,7 +2377,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     if (e == hipSuccess) {
       hipLaunchKernelGGL(prepare_tables_kernel, dim3(256, d->num_thetas), dim3(256), 0, 0,
                          d->d_cos, d->d_sin, p->d_cos, p->d_sin, p->d_ucos, p->d_usin, D / 2,
-                         static_cast<int64_t>(d->table_positions) * (D / 2), padded_positions * (D / 2), d_norm);
+                         static_cast<int64_t>(d->table_positions) * (D / 2), padded_positions * (D / 2), d_norm,
+                         p->generic ? 1 : 0);
       e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipMemcpy(norm.data(), d_norm, norm.size() * sizeof(unsigned), hipMemcpyDeviceToHost);
@@ -2221,7 +2412,10 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   hipError_t e = hipMemcpy(d_order, order.data(), order.size() * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
     uint16_t* wp = static_cast<uint16_t*>(p->d_w);
-    if (D == 64 && p->ntw == 2)
+    if (p->generic)
+      hipLaunchKernelGGL(copy_weights_kernel, dim3(1024), dim3(256), 0, 0, d->d_weight, d->d_bias, d_order,
+                         nj, S * D * D, D, static_cast<float*>(p->d_w), p->d_bias);
+    else if (D == 64 && p->ntw == 2)
       launch_pack<64, 2>(d, d_order, wp, p->d_bias);
     else if (D == 64)
       launch_pack<64, 3>(d, d_order, wp, p->d_bias);
@@ -2243,7 +2437,7 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   p->info.num_groups = static_cast<int32_t>(group_unit_start.size());
   p->info.num_thetas = d->num_thetas;
   p->info.table_positions = d->table_positions;
-  p->info.weight_terms = p->ntw;
+  p->info.weight_terms = p->generic ? 1 : p->ntw;
   p->info.device_bytes = bytes;
   return CB_OK;
 }
@@ -2251,6 +2445,7 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
 // Default tokens per workgroup: about three workgroups per CU over the launch
 // (one resident per CU for the streaming kernel), at least 512 tokens.
 int default_chunk(const cb_plan* p, int n) {
+  if (p->generic) return 8 * kAnyTile;
   if (p->info.support != 1) return kGenSubTokens;
   int64_t units = 0;
   for (int c = 0; c < p->num_windows; ++c) units += p->cls_unit_end[c] - p->cls_unit_begin[c];
@@ -2377,8 +2572,8 @@ void split_cost_line(const cb_plan* p, MapArgs* a) {
 int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t* count,
                int tokens_per_workgroup, int default_tokens, hipStream_t s) {
   const int D = p->info.head_dim;
-  const bool ws = p->info.support == 1;
-  const int unit = ws ? kSubTokens : kGenSubTokens;
+  const bool ws = p->info.support == 1 && !p->generic;
+  const int unit = p->generic ? kAnyTile : ws ? kSubTokens : kGenSubTokens;
   int chunk = tokens_per_workgroup > 0 ? tokens_per_workgroup : default_tokens;
   if (tokens_per_workgroup < 0 || chunk < unit || chunk % unit)
     return fail(CB_EINVAL, "tokens_per_workgroup must be a positive multiple of %d", unit);
@@ -2467,6 +2662,11 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
       if (pv) hipLaunchKernelGGL((map_install_stream_kernel<64, float, true>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((map_install_stream_kernel<64, float, false>), grid, block, 0, s, a);
     }
+  } else if (p->generic) {
+    const dim3 g(static_cast<unsigned>(grid_blocks)), b(kAnyThreads);
+    if (p->info.io_dtype == CB_DTYPE_BF16) hipLaunchKernelGGL(map_install_any_kernel<uint16_t>, g, b, 0, s, a, D);
+    else if (p->info.io_dtype == CB_DTYPE_F16) hipLaunchKernelGGL(map_install_any_kernel<_Float16>, g, b, 0, s, a, D);
+    else hipLaunchKernelGGL(map_install_any_kernel<float>, g, b, 0, s, a, D);
   } else if (p->support_gemm) {
     // One persistent workgroup per CU; 8 per XCD at least.
     const unsigned per_xcd = static_cast<unsigned>(std::max(1, p->num_cus / 8));
@@ -2576,12 +2776,11 @@ int cb_plan_create(const cb_plan_desc* d, cb_plan** out) {
   if (!d || !out) return fail(CB_EINVAL, "null descriptor or output");
   *out = nullptr;
   const int D = d->head_dim, S = d->support, nj = d->num_jobs;
-  if (D != 64 && D != 128) return fail(CB_EINVAL, "head_dim must be 64 or 128 (got %d)", D);
+  if (D < 2 || D > kAnyMaxDim || (D & 1))
+    return fail(CB_EINVAL, "head_dim must be even and in [2, %d] (got %d)", kAnyMaxDim, D);
   if (S < 1 || S > CB_MAX_SUPPORT) return fail(CB_EINVAL, "support must be in [1, %d]", CB_MAX_SUPPORT);
-  if (d->io_dtype != CB_DTYPE_BF16 && d->io_dtype != CB_DTYPE_F32)
-    return fail(CB_EINVAL, "io_dtype must be CB_DTYPE_BF16 or CB_DTYPE_F32");
-  if (d->io_dtype == CB_DTYPE_F32 && D != 64)
-    return fail(CB_EINVAL, "fp32 I/O is supported for head_dim 64 only");
+  if (d->io_dtype != CB_DTYPE_BF16 && d->io_dtype != CB_DTYPE_F32 && d->io_dtype != CB_DTYPE_F16)
+    return fail(CB_EINVAL, "io_dtype must be CB_DTYPE_BF16, CB_DTYPE_F16 or CB_DTYPE_F32");
   if (nj < 1 || d->target_layers < 1 || d->target_heads < 1)
     return fail(CB_EINVAL, "num_jobs, target_layers and target_heads must be positive");
   if (nj > (1 << 20)) return fail(CB_EINVAL, "too many jobs");
@@ -2690,8 +2889,9 @@ int cb_map_install(const cb_plan* p, const cb_request* rq, void* stream) {
   int rc;
   if ((rc = check_sides(p, sr, tr))) return rc;
   MapArgs a{};
-  if ((rc = to_dev_rows(sr, p->elem_bytes, &a.src))) return rc;
-  if ((rc = to_dev_rows(tr, p->elem_bytes, &a.tgt))) return rc;
+  const int align = p->generic ? p->elem_bytes : 16;
+  if ((rc = to_dev_rows(sr, p->elem_bytes, &a.src, align))) return rc;
+  if ((rc = to_dev_rows(tr, p->elem_bytes, &a.tgt, align))) return rc;
   const int64_t prefix = rq->prefix_length > 0 ? rq->prefix_length
                                                : static_cast<int64_t>(rq->position_start) + n;
   if (prefix < static_cast<int64_t>(rq->position_start) + n)
@@ -2721,8 +2921,9 @@ int cb_map_install_batch(const cb_plan* p, const cb_rows* source, const cb_rows*
   if (source->rows > INT32_MAX || target->rows > INT32_MAX)
     return fail(CB_EINVAL, "batched launches address at most 2^31 rows per side");
   BatchArgs b{};
-  if ((rc = to_dev_rows(*source, p->elem_bytes, &b.src))) return rc;
-  if ((rc = to_dev_rows(*target, p->elem_bytes, &b.tgt))) return rc;
+  const int align = p->generic ? p->elem_bytes : 16;
+  if ((rc = to_dev_rows(*source, p->elem_bytes, &b.src, align))) return rc;
+  if ((rc = to_dev_rows(*target, p->elem_bytes, &b.tgt, align))) return rc;
   BatchLayout L;
   if ((rc = batch_layout(p, spans, num_spans, &L))) return rc;
   for (int r = 0; r < num_spans; ++r) {
@@ -2810,8 +3011,9 @@ int cb_map_install_batch_noalloc(const cb_plan* p, const cb_rows* source, const 
 int cb_copy_rows(const cb_rows* src, const cb_rows* dst, int32_t num_layers, int32_t num_tokens,
                  int32_t row_elements, int32_t dtype, int32_t* d_error_flag, void* stream) {
   if (!src || !dst) return fail(CB_EINVAL, "null rows");
-  if (dtype != CB_DTYPE_BF16 && dtype != CB_DTYPE_F32) return fail(CB_EINVAL, "bad dtype");
-  const int eb = dtype == CB_DTYPE_BF16 ? 2 : 4;
+  if (dtype != CB_DTYPE_BF16 && dtype != CB_DTYPE_F32 && dtype != CB_DTYPE_F16)
+    return fail(CB_EINVAL, "bad dtype");
+  const int eb = dtype == CB_DTYPE_F32 ? 4 : 2;
   if (num_layers < 1 || num_tokens < 0 || row_elements < 1)
     return fail(CB_EINVAL, "num_layers and row_elements must be positive");
   if ((static_cast<int64_t>(row_elements) * eb) % 16)

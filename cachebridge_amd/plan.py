@@ -19,14 +19,15 @@ import torch
 from . import _lib
 from .rope import rope_tables
 
-_DTYPES = {torch.bfloat16: _lib.CB_DTYPE_BF16, torch.float32: _lib.CB_DTYPE_F32}
+_DTYPES = {torch.bfloat16: _lib.CB_DTYPE_BF16, torch.float16: _lib.CB_DTYPE_F16,
+           torch.float32: _lib.CB_DTYPE_F32}
 
 
 def io_dtype_code(dtype: torch.dtype) -> int:
     try:
         return _DTYPES[dtype]
     except KeyError:
-        raise ValueError(f"unsupported KV dtype {dtype}; expected bfloat16 or float32") from None
+        raise ValueError(f"unsupported KV dtype {dtype}; expected bfloat16, float16 or float32") from None
 
 
 @dataclass

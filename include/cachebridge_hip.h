@@ -58,6 +58,7 @@ extern "C" {
 #define CB_DTYPE_BF16 0
 #define CB_DTYPE_F32 1
 #define CB_DTYPE_F64 2 /* cb_delta_state_transform only */
+#define CB_DTYPE_F16 3 /* map / install / row copy I/O */
 
 /* Job kinds. */
 #define CB_KIND_K 0
@@ -110,7 +111,9 @@ typedef struct cb_rows {
  * support rows in pair order) plus a [head_dim] fp32 bias.
  */
 typedef struct cb_plan_desc {
-  int32_t head_dim;  /* 64 or 128 */
+  int32_t head_dim;  /* even, 2..512. bf16 at 64 and 128 and fp32 at 64 take the
+                        MFMA kernels; every other head_dim or dtype takes the
+                        generic fp32 kernel (same results within the parity bar) */
   int32_t support;   /* 1..CB_MAX_SUPPORT */
   int32_t io_dtype;  /* CB_DTYPE_* */
   int32_t num_jobs;

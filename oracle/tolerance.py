@@ -8,8 +8,8 @@ the contraction in a different order differs from ``y`` by
 ``|dy| <= c * u * sum_i |x_i w_i|`` (standard dot-product forward error,
 ``u`` the working precision), so an elementwise "<= 1 bf16 ulp" can only
 hold where ``|y|`` is not much smaller than that sum. ``check_mapped``
-therefore accepts an element when its bf16 bit patterns are at most one ulp
-apart **or** ``|out - ref| <= abs_factor * bound``, where ``bound`` is the
+therefore accepts an element when its bf16 (or fp16, for fp16 pools) bit
+patterns are at most one ulp apart **or** ``|out - ref| <= abs_factor * bound``, where ``bound`` is the
 magnitude of the chain's summands (``magnitude_bound``), and separately
 requires a normwise relative error ``max|out-ref| / max|ref| <= 1e-2``.
 """
@@ -21,14 +21,24 @@ import torch
 from .rope import qwen_rope
 
 
-def bf16_ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """Distance in representable bf16 steps between equal-shape bf16 tensors."""
+def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in representable steps between equal-shape bf16 or fp16 tensors.
+
+    Both formats are sign-magnitude 16-bit patterns whose magnitudes order as
+    integers, so the distance is the difference of the signed-magnitude
+    integers (+0 and -0 are 0 apart).
+    """
 
     def ordered(x):
         i = x.contiguous().view(torch.int16).to(torch.int32)
         return torch.where(i < 0, -(i & 0x7FFF), i)
 
     return (ordered(a) - ordered(b)).abs()
+
+
+def bf16_ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in representable bf16 steps between equal-shape bf16 tensors."""
+    return ulp_distance(a, b)
 
 
 def magnitude_bound(page: torch.Tensor, spec: dict, *, position_start: int, source_theta: float,
@@ -83,8 +93,8 @@ def check_mapped(out: torch.Tensor, ref: torch.Tensor, bound: torch.Tensor, *,
     allowed = diff <= abs_factor * bound
     stats = {"elements": o.numel(), "max_abs": float(diff.max()),
              "rel_norm": float(diff.max() / r.double().abs().max().clamp_min(1e-30))}
-    if o.dtype == torch.bfloat16:
-        ulp = bf16_ulp_distance(o, r)
+    if o.dtype in (torch.bfloat16, torch.float16):
+        ulp = ulp_distance(o, r)
         within = ulp <= 1
         stats["within_1ulp"] = float(within.double().mean())
         stats["max_ulp"] = int(ulp.max())

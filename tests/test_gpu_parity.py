@@ -241,3 +241,83 @@ def test_support_items_ignore_tokens_per_workgroup():
     for a_, b_ in zip(first, bufs):
         assert torch.equal(a_, b_)
     assert all(bool(b.abs().sum() > 0) for b in first)
+
+
+@pytest.mark.parametrize("dim,dtype,support", [(96, torch.bfloat16, 1), (256, torch.bfloat16, 2),
+                                               (80, torch.float16, 1), (128, torch.float32, 1),
+                                               (6, torch.bfloat16, 3), (512, torch.float16, 1),
+                                               (128, torch.float16, 2)])
+def test_generic_head_dims_and_dtypes_match_oracle(dim, dtype, support):
+    """Head dims and dtypes outside the MFMA kernels' (bf16 at 64 / 128, fp32
+    at 64) run on the generic fp32 kernel: map_page against the oracle."""
+    print(f"generic map D={dim} {dtype} s={support}", flush=True)
+    g = torch.Generator().manual_seed(17 + dim + support)
+    ls, hs, lt, ht, n, p0 = 6, 2, 3, 2, 70, 123
+    layers = torch.stack([torch.randperm(ls, generator=g)[:support] for _ in range(lt * ht)])
+    spec = {"assign_layer": layers.view(lt, ht, support),
+            "assign_head": torch.randint(0, hs, (lt, ht, support), generator=g),
+            "k_weight": torch.randn(lt, ht, support * dim, dim, generator=g) / (support * dim) ** 0.5,
+            "v_weight": torch.randn(lt, ht, support * dim, dim, generator=g) / (support * dim) ** 0.5,
+            "k_bias": torch.randn(lt, ht, dim, generator=g) * 0.1,
+            "v_bias": torch.randn(lt, ht, dim, generator=g) * 0.1}
+    mapper = HeadwiseMapper.from_assignment(**spec, source_rope_theta=1e4, target_rope_theta=1e6, dtype=dtype,
+                                            device="cuda", max_positions=2048)
+    assert mapper.plan.info["weight_terms"] == 1  # the generic plan keeps fp32 maps
+    page = torch.randn(2, ls, n, hs, dim, generator=g).to(dtype)
+    out = mapper.map_page(page.cuda(), position_start=p0, output_device="cuda")
+    virtual = oi.virtual_source_page(page, spec["assign_layer"], spec["assign_head"])
+    ref = oi.assignment_mapper(spec, source_rope_theta=1e4, target_rope_theta=1e6).map_page(
+        virtual, position_start=p0)
+    bound = ot.magnitude_bound(page, spec, position_start=p0, source_theta=1e4, target_thetas=1e6)
+    print(ot.check_mapped(out, ref, bound, abs_factor=_factor(dtype)), flush=True)
+
+
+def _generic_shape(tokens):
+    return synthetic.Shape("generic96", 8, 2, 6, 2, 96, tokens, torch.bfloat16, [1, 3, 5, 6],
+                           target_theta=[1e6, 1e4, 1e4, 1e6, 1e4, 1e4],
+                           windows=[None, 64, 64, None, 64, 64], target_pages=64, seed=3)
+
+
+def test_generic_pool_install_with_windows_matches_oracle():
+    """The generic kernel's paged install: windowed layers, two thetas, block
+    table; untouched rows bit-exact, mapped rows within the parity bar."""
+    print("generic pool install D=96", flush=True)
+    sh = _generic_shape(300)
+    h = synthetic.make_handoff(sh, target_pages=64, fill_target=None)
+    torch.manual_seed(0)
+    h.target_pool.k_data.copy_(torch.randn_like(h.target_pool.k_data, dtype=torch.float32))
+    h.target_pool.v_data.copy_(torch.randn_like(h.target_pool.v_data, dtype=torch.float32))
+    before = _cpu_pool(h.target_pool)
+    h.run()
+    assert h.mapper.plan.read_errors() == 0
+    mapped, tgt_slots = _oracle_install(h, before)
+    _check_pools(h, before, mapped, tgt_slots)
+
+
+def test_generic_batch_equals_per_request_installs():
+    print("generic batch D=96", flush=True)
+    from cachebridge_amd.pool import pool_rows
+
+    lengths = [40, 100, 17]
+    sh = _generic_shape(sum(lengths))
+    b = synthetic.make_batch_handoff(sh, lengths, occupancy=0.5)
+    pool = b.target_pool
+    pool.k_data.zero_()
+    pool.v_data.zero_()
+    b.run()
+    torch.cuda.synchronize()
+    batched = (pool.k_data.clone(), pool.v_data.clone())
+    pool.k_data.zero_()
+    pool.v_data.zero_()
+    ps = sh.page_size
+    for sp in b.spans:
+        e = sp.target_offset // ps
+        src = pool_rows(b.source_pool, index=b.source_slots, index_offset=sp.source_offset, tokens=sp.num_tokens)
+        tgt = pool_rows(pool, block_table=b.block_table[e:e + (sp.num_tokens + ps - 1) // ps], page_size=ps,
+                        tokens=sp.num_tokens)
+        b.mapper.map_install(src, tgt, num_tokens=sp.num_tokens, position_start=sp.position_start,
+                             prefix_length=sp.prefix_length)
+    torch.cuda.synchronize()
+    assert b.mapper.plan.read_errors() == 0
+    assert torch.equal(pool.k_data, batched[0]) and torch.equal(pool.v_data, batched[1])
+    assert bool(batched[0].abs().sum() > 0)

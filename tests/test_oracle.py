@@ -215,3 +215,32 @@ def test_tolerance_accepts_one_ulp_and_rejects_two():
     two = (bits + 2).view(torch.bfloat16)
     with pytest.raises(AssertionError):
         ot.check_mapped(two, ref, tiny)
+
+
+@pytest.mark.parametrize("dtype,mant", [(torch.bfloat16, 7), (torch.float16, 10)])
+def test_ulp_distance_counts_representable_steps(dtype, mant):
+    """One step up from a normal x is 2^(floor(log2|x|) - mantissa bits); the
+    distance counts steps across zero (+0 and -0 coincide)."""
+    x = torch.tensor([1.0, 2.5, 3e-3, 700.0, 0.75], dtype=dtype)
+    up = (x.view(torch.int16) + 1).view(dtype)
+    step = up.double() - x.double()
+    expect = torch.exp2(torch.floor(torch.log2(x.double())) - mant)
+    assert torch.equal(step, expect)
+    assert ot.ulp_distance(up, x).tolist() == [1] * 5
+    three = (x.view(torch.int16) + 3).view(dtype)
+    assert ot.ulp_distance(three, x).tolist() == [3] * 5
+    zeros = torch.tensor([0.0, -0.0], dtype=dtype)
+    assert ot.ulp_distance(zeros[:1], zeros[1:]).item() == 0
+    tiny = torch.tensor([1], dtype=torch.int16).view(dtype)   # smallest positive
+    neg = torch.tensor([-32767], dtype=torch.int16).view(dtype)  # bits 0x8001: smallest negative
+    assert ot.ulp_distance(tiny, neg).item() == 2
+
+
+def test_tolerance_accepts_one_fp16_ulp_and_rejects_two():
+    g = torch.Generator().manual_seed(6)
+    ref = (torch.randn(2, 1, 32, 2, 96, generator=g) * 3).to(torch.float16)
+    bits = ref.view(torch.int16)
+    tiny = torch.zeros(ref.shape, dtype=torch.float64)
+    ot.check_mapped((bits + 1).view(torch.float16), ref, tiny, min_within_ulp=1.0)
+    with pytest.raises(AssertionError):
+        ot.check_mapped((bits + 2).view(torch.float16), ref, tiny)
