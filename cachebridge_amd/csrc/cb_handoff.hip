@@ -939,49 +939,52 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
 //
 // A target job's feature row is the concatenation of its s source rows, so
 // each job is a [T x s*128] . [s*128 x 128] contraction (the shipped top-8
-// recipe: 1024 input dims). An item is one 128-token block of one job. The
-// input dims of an item are streamed in 2*s stages of 64 dims -- k-step pair
-// {q, q + 2} (32 first-half dims and their RoPE partners) of support member
-// k, all members for q = 0 first.
+// recipe: 1024 input dims). An item is one 256-token block of one job. Its
+// input dims stream through LDS one k-step (32 dims) per stage, 4*s stages:
+// for q = 0, 1 and each support member k, k-step q (32 first-half dims)
+// then k-step q + 2 (their RoPE partners).
 //
-// One persistent workgroup of 8 waves per CU. Waves 4..7 produce, waves
-// 0..3 consume, through a ring of two LDS stage buffers (W of the stage: 8
-// row tiles x 2 k-steps x 2 terms, 32 KB; the stage's input: 128 tokens x 64
+// One persistent workgroup of 8 waves per CU, a ring of three stage buffers
+// (W of the k-step: 8 row tiles x 2 terms, 16 KB; the input: 256 tokens x 32
 // dims x 2 terms, 32 KB):
-//   - a producer wave waits until the consumers have released the buffer,
-//     writes its quarter of the stage's W (loaded two stages ahead into
-//     registers) and of its input (loaded two stages ahead; keys un-rotated
-//     and split into bf16 terms, values written as loaded), signals the
-//     buffer full, and requests the loads of the stage after next, which may
-//     belong to the next item;
-//   - consumer wave (h, c) waits until all four producers have filled the
-//     buffer, multiplies row tiles {h*2 + q', +4} (an output half with its
-//     RoPE partners) by column tiles 4c .. 4c + 3 (64 tokens) into 64
-//     accumulator VGPRs, releases the buffer, and after an item's last stage
-//     runs the epilogue (bias as the first accumulator input, target RoPE,
-//     cast, stores of whole 64-byte chunks of the target rows).
-// Full and empty are monotonic per-buffer counters in LDS (a producer wave
-// adds 1 when its writes are done, a consumer wave adds 1 when its reads are
-// done), so no workgroup barrier is needed after start-up and the loads in
-// flight are never drained. LDS executes one wave's operations in order, so
-// data written before a counter update is visible to a wave that has seen the
-// update. Every wait is bounded: after about a second without progress a wave
-// flags the error word and sets a workgroup abort flag that ends every other
-// wait, so no launch can hang.
+//   - producer waves 4..7 work on k-step pairs {q, q + 2} of one member:
+//     with the pair's W and source dims in registers (requested one pair
+//     ahead), they un-rotate keys and split both halves into bf16 terms,
+//     write the first stage as soon as its buffer is free and signal, hold
+//     the second stage's terms in registers until the next buffer is free,
+//     write and signal it. Producer wave pw holds W fragments of one k-step
+//     and term (k-step slot pw >> 1, term pw & 1) for all 8 row tiles, so
+//     waves 4, 5 write W of the first stage and waves 6, 7 of the second;
+//   - consumer wave (h, c) waits until all four producers have signalled a
+//     stage, multiplies row tiles {h*2 + q', +4} (an output half with its
+//     RoPE partners) by column tiles 8c .. 8c + 7 (128 tokens) into 128
+//     accumulator VGPRs, releases the buffer, and after an item's last
+//     stage runs the epilogue (bias as the first accumulator input, target
+//     RoPE, cast, stores of whole 64-byte chunks of the target rows).
+// Full and empty are monotonic per-buffer counters in LDS (each of the four
+// producer waves adds 1 when its part of a stage is written, each consumer
+// wave adds 1 when its reads of the stage are done), so no workgroup barrier
+// is needed after start-up and the loads in flight are never drained. LDS
+// executes one wave's operations in order, so data written before a counter
+// update is visible to a wave that has seen the update. Every wait is
+// bounded: after about a third of a second without progress a wave flags the
+// error word and sets a workgroup abort flag that ends every other wait, so
+// no launch can hang.
 //
 // Items: the jobs of each window class are dealt to the 8 XCDs round-robin
 // (job j of a class to XCD j % 8, keys and values alike), each XCD's items
 // are its jobs' blocks in order, and the workgroups of an XCD take every
 // (workgroups per XCD)-th item of that list. The workgroups of one XCD then
-// run the blocks of one job at a time and read its W (512 KB at s = 8) from
-// their shared L2, and every XCD gets the same mix of key and value jobs.
+// run the blocks of one or two jobs at a time and read their W (512 KB at
+// s = 8) from their shared L2, and every XCD gets the same key/value mix.
 // W is packed with the group output permutation (grp_out_dim).
 // ---------------------------------------------------------------------------
 
-constexpr int kSupTile = 128;                 // tokens per item
+constexpr int kSupTile = 256;                 // tokens per item
 constexpr int kSupWaves = 8;                  // 4 consumer and 4 producer waves
 constexpr int kSupThreads = kSupWaves * kWave;
 constexpr int kSupRoleWaves = 4;
+constexpr int kSupRing = 3;
 
 // Output dim of row r (0..15) of row tile rt (0..7): tile rt = p*4 + h*2 + q
 // holds in lane group g = r / 4 the dims p*64 + h*32 + g*8 + q*4 + r % 4, so
@@ -992,20 +995,20 @@ __host__ __device__ inline int grp_out_dim(int rt, int r) {
   return (rt >> 2) * 64 + ((rt >> 1) & 1) * 32 + (r >> 2) * 8 + (rt & 1) * 4 + (r & 3);
 }
 
-// One stage buffer: W [row tile][k-step][term][lane] (32 KB) and the input
-// [column tile][k-step][term][lane] (32 KB).
+// One stage buffer: W [row tile][term][lane] (16 KB) and the input
+// [column tile][term][lane] (32 KB) of one k-step.
 struct SupStage {
-  uint4 w[8][2][2][kWave];
-  uint4 x[8][2][2][kWave];
+  uint4 w[8][2][kWave];
+  uint4 x[16][2][kWave];
 };
 
 struct SupShared {
-  SupStage ring[2];
+  SupStage ring[kSupRing];
   int32_t trow[2][kSupTile];  // [item parity]: target row per token (-1: write nothing)
   int32_t tpos[2][kSupTile];  // [item parity]: target position per token
   float bias[2][128];         // [item parity]
-  uint32_t full[2];           // producer-wave fills of each buffer
-  uint32_t empty[2];          // consumer-wave releases of each buffer
+  uint32_t full[kSupRing];    // producer-wave fills of each buffer
+  uint32_t empty[kSupRing];   // consumer-wave releases of each buffer
   uint32_t abort;             // set when a wait timed out
 };
 
@@ -1070,19 +1073,19 @@ __device__ inline void sup_signal(uint32_t* ctr) {
 // Producer's view of an item: what its loads and its LDS side tables need.
 struct SupLoad {
   bool valid, is_k;
-  int nstage;
+  int npair;            // k-step pairs of the item: 2 * support
   gcptr wjob;           // the job's packed W, + lane * 16
   const int32_t* pj;    // the job's support pairs
   int kind;
-  int64_t soff[2];      // per task: source row byte offset, -1 for the zero row
-  int pos[2];           // per task: source position
+  int64_t soff[4];      // per task: source row byte offset, -1 for the zero row
+  int pos[4];           // per task: source position
   const CB_GLOBAL float* ucos;
   const CB_GLOBAL float* usin;
 };
 
-// Producer thread pt (0..255) of wave pw: tasks j = 0, 1 are column tile
-// 2 * pw + j, token 16 * (2 * pw + j) + (lane & 15), first-half dims
-// 16g + 8q .. +7 (g = lane >> 4) and their partners.
+// Producer thread (wave pw, lane): tasks j = 0..3 are column tile 4 * pw + j,
+// token 16 * (4 * pw + j) + (lane & 15), first-half dims 16g + 8q .. +7
+// (g = lane >> 4) and their partners.
 __device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems::Item& it, int parity,
                                   int pw, SupLoad& L) {
   constexpr int D = 128;
@@ -1093,7 +1096,7 @@ __device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems
   L.valid = true;
   L.kind = meta_y & 0xff;
   L.is_k = L.kind == CB_KIND_K;
-  L.nstage = 2 * a.support;
+  L.npair = 2 * a.support;
   L.wjob = as_global(a.w + static_cast<size_t>(it.job) * a.support * Gm<128, uint16_t>::W_U4) + lane * 16;
   L.pj = a.pairs + static_cast<size_t>(it.job) * a.support;
   const int sth = (meta_y >> 16) & 0xff;
@@ -1102,8 +1105,8 @@ __device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems
   L.usin = gtab(shared ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
   const int n = it.hi - it.lo;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int pt = 16 * (2 * pw + j) + col;
+  for (int j = 0; j < 4; ++j) {
+    const int pt = 16 * (4 * pw + j) + col;
     const int tk = it.lo + min(pt, n - 1);
     const bool live = pt < n;
     const int64_t srow = row_of(a.src, tk);
@@ -1123,22 +1126,20 @@ __device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems
   if (pt < D) S.bias[parity][pt] = a.bias[static_cast<size_t>(it.job) * D + pt];
 }
 
-// Loads of stage t of item L: W fragments (f = j * 4 + pw: row tile f >> 2,
-// k-step slot (f >> 1) & 1, term f & 1).
+// W of k-step pair t (member k = t % S, q = t / S): the 8 row tiles of
+// k-step slot pw >> 1 (q or q + 2) and term pw & 1.
 __device__ inline void sup_issue_w(const MapArgs& a, const SupLoad& L, int t, int pw, uint4 (&w)[8]) {
   const int S = a.support;
   const int q = t >= S ? 1 : 0, k = t - q * S;
+  const int ks = q + 2 * (pw >> 1), tm = pw & 1;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int f = j * kSupRoleWaves + pw;
-    const int rt = f >> 2, kk = (f >> 1) & 1, tm = f & 1;
-    const int ks = q + 2 * kk;
-    w[j] = gload<uint4>(L.wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
-  }
+  for (int rt = 0; rt < 8; ++rt)
+    w[rt] = gload<uint4>(L.wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
 }
 
-// Loads of stage t of item L: the two tasks' source dims and their partners.
-__device__ inline void sup_issue_x(const MapArgs& a, const SupLoad& L, int t, uint4 (&x)[2][2]) {
+// Source dims of k-step pair t for the four tasks: 8 first-half dims and
+// their partners each.
+__device__ inline void sup_issue_x(const MapArgs& a, const SupLoad& L, int t, uint4 (&x)[4][2]) {
   constexpr int HALF = 64;
   const int S = a.support;
   const int g = (threadIdx.x & (kWave - 1)) >> 4;
@@ -1147,18 +1148,18 @@ __device__ inline void sup_issue_x(const MapArgs& a, const SupLoad& L, int t, ui
   gcptr base = layer_base(a.src, L.kind, pr & 0xffff) + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * 128 * 2;
   gcptr zrow = as_global(a.zero);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < 4; ++j) {
     gcptr p = (L.soff[j] >= 0 ? base + L.soff[j] : zrow) + (16 * g + 8 * q) * 2;
     x[j][0] = gload<uint4>(p);
     x[j][1] = gload<uint4>(p + HALF * 2);
   }
 }
 
-// Un-rotation values of both tasks of item L for k-step pair q.
-__device__ inline void sup_issue_tab(const SupLoad& L, int q, float (&c)[2][8], float (&s)[2][8]) {
+// Un-rotation values of the four tasks of item L for k-step pair q.
+__device__ inline void sup_issue_tab(const SupLoad& L, int q, float (&c)[4][8], float (&s)[4][8]) {
   const int g = (threadIdx.x & (kWave - 1)) >> 4;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int64_t off = tab_chunk<16>(L.pos[j], 2 * q + u, g);
@@ -1169,101 +1170,128 @@ __device__ inline void sup_issue_tab(const SupLoad& L, int q, float (&c)[2][8], 
     }
 }
 
-// Producer side of the whole launch (waves 4..7). Per stage n: wait for the
-// buffer, write W and the input (both loaded two stages ahead; the input
-// un-rotated with values loaded one stage ahead), signal, then request
-// the un-rotation values of stage n + 1 and W and the input of stage n + 2.
-// L is the item of the W and input loads; stage n + 1 always belongs to it
-// before it moves on.
+// Producer side of the whole launch (waves 4..7). L is the item of the
+// loads, which run one k-step pair ahead of the production (and so move to
+// the next item one pair before the producing item ends).
 __device__ void sup_producer(const MapArgs& a, SupShared& S, SupItems items) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & (kWave - 1);
   const int pw = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) - kSupRoleWaves;
   const int Sup = a.support;
-  const int nstage = 2 * Sup;
+  const int npair = 2 * Sup;
   SupItems::Item it;
   if (!items.get(a, it)) return;
   SupLoad L;
   int load_parity = 0;
   sup_decode(a, S, it, 0, pw, L);
-  uint4 wa[8], wb[8], xa[2][2], xb[2][2];
-  float tc[2][8], ts[2][8];
-  sup_issue_w(a, L, 0, pw, wa);
+  uint4 w[8], x[4][2];
+  float tc[4][8], ts[4][8];
+  sup_issue_w(a, L, 0, pw, w);
   if (L.is_k) sup_issue_tab(L, 0, tc, ts);
-  sup_issue_x(a, L, 0, xa);
-  sup_issue_w(a, L, 1, pw, wb);
-  sup_issue_x(a, L, 1, xb);
-  int lt = 2;       // stage of L the next input loads are for
+  sup_issue_x(a, L, 0, x);
+  int lt = 1;       // pair of L the next loads are for
   uint32_t n = 0;   // global stage index
   bool p_is_k = L.is_k;
+  const bool w_first = pw < 2;  // this wave's W fragments belong to the pair's first stage
 
-  auto produce = [&](int t, uint4 (&w)[8], uint4 (&x)[2][2]) {
-    const int slot = n & 1;
-    sup_wait(S, &S.empty[slot], 4 * (n >> 1), a.err);
-    SupStage& B = S.ring[slot];
+  auto put_w = [&](SupStage& B) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int f = j * kSupRoleWaves + pw;
-      B.w[f >> 2][(f >> 1) & 1][f & 1][lane] = w[j];
+    for (int rt = 0; rt < 8; ++rt) B.w[rt][pw & 1][lane] = w[rt];
+  };
+
+  // Requests the next pair's loads (advancing L at its end); ``part`` 0
+  // requests the source dims (and W when this wave's W went out with the
+  // first stage), part 1 the rest of W.
+  bool next_valid = true;
+  int next_t = 0;
+  auto advance = [&]() {
+    if (!L.valid) {
+      next_valid = false;
+      return;
     }
-    if (p_is_k) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int ct = 2 * pw + j;
-        float x1[8], x2[8];
-        unpack16<uint16_t>(x[j][0], x1);
-        unpack16<uint16_t>(x[j][1], x2);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float k1 = __builtin_fmaf(x1[e], tc[j][e], x2[e] * ts[j][e]);
-          const float k2 = __builtin_fmaf(x2[e], tc[j][e], -(x1[e] * ts[j][e]));
-          x1[e] = k1;
-          x2[e] = k2;
-        }
-        uint32_t t1[2][4], t2[2][4];
-        split_terms<2, 8>(x1, t1);
-        split_terms<2, 8>(x2, t2);
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-          B.x[ct][0][v][lane] = make_uint4(t1[v][0], t1[v][1], t1[v][2], t1[v][3]);
-          B.x[ct][1][v][lane] = make_uint4(t2[v][0], t2[v][1], t2[v][2], t2[v][3]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int ct = 2 * pw + j;
-        B.x[ct][0][0][lane] = x[j][0];
-        B.x[ct][1][0][lane] = x[j][1];
-      }
-    }
-    sup_signal(&S.full[slot]);
-    ++n;
-    if (!L.valid) return;
-    // Stage n (the next one) is stage lt - 1 of L.
-    const int tn = lt - 1;
-    if (tn < nstage && L.is_k && (tn == 0 || tn == Sup)) sup_issue_tab(L, tn == 0 ? 0 : 1, tc, ts);
-    if (lt == nstage) {
+    if (lt == npair) {
       items.next += items.nwg;
       if (!items.get(a, it)) {
         L.valid = false;
+        next_valid = false;
         return;
       }
       load_parity ^= 1;
       sup_decode(a, S, it, load_parity, pw, L);
       lt = 0;
     }
-    sup_issue_w(a, L, lt, pw, w);
-    sup_issue_x(a, L, lt, x);
+    next_t = lt;
     ++lt;
-    (void)t;
   };
 
   SupItems prod = items;  // the producing item (behind L by at most one)
   for (;;) {
-    for (int t = 0; t < nstage; t += 2) {
-      produce(t, wa, xa);
-      produce(t + 1, wb, xb);
+    for (int t = 0; t < npair; ++t) {
+      // Both stages' input terms of this pair, from x (and the un-rotation
+      // values of its q, requested one pair ahead).
+      uint4 xa[4][2], xb[4][2];  // [task][term]: first stage (q), second stage (q + 2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (p_is_k) {
+          float x1[8], x2[8];
+          unpack16<uint16_t>(x[j][0], x1);
+          unpack16<uint16_t>(x[j][1], x2);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float k1 = __builtin_fmaf(x1[e], tc[j][e], x2[e] * ts[j][e]);
+            const float k2 = __builtin_fmaf(x2[e], tc[j][e], -(x1[e] * ts[j][e]));
+            x1[e] = k1;
+            x2[e] = k2;
+          }
+          uint32_t t1[2][4], t2[2][4];
+          split_terms<2, 8>(x1, t1);
+          split_terms<2, 8>(x2, t2);
+#pragma unroll
+          for (int v = 0; v < 2; ++v) {
+            xa[j][v] = make_uint4(t1[v][0], t1[v][1], t1[v][2], t1[v][3]);
+            xb[j][v] = make_uint4(t2[v][0], t2[v][1], t2[v][2], t2[v][3]);
+          }
+        } else {
+          xa[j][0] = x[j][0];
+          xb[j][0] = x[j][1];
+          xa[j][1] = xb[j][1] = make_uint4(0, 0, 0, 0);
+        }
+      }
+      // The source and table registers are free: request the next pair's
+      // source dims, and its un-rotation values when its q starts (keys).
+      advance();
+      if (next_valid) sup_issue_x(a, L, next_t, x);
+      if (next_valid && L.is_k && (next_t == 0 || next_t == Sup)) sup_issue_tab(L, next_t == 0 ? 0 : 1, tc, ts);
+      // First stage (k-step q).
+      {
+        const int slot = n % kSupRing;
+        sup_wait(S, &S.empty[slot], 4 * (n / kSupRing), a.err);
+        SupStage& B = S.ring[slot];
+        if (w_first) put_w(B);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          B.x[4 * pw + j][0][lane] = xa[j][0];
+          if (p_is_k) B.x[4 * pw + j][1][lane] = xa[j][1];
+        }
+        sup_signal(&S.full[slot]);
+        ++n;
+      }
+      if (w_first && next_valid) sup_issue_w(a, L, next_t, pw, w);
+      // Second stage (k-step q + 2).
+      {
+        const int slot = n % kSupRing;
+        sup_wait(S, &S.empty[slot], 4 * (n / kSupRing), a.err);
+        SupStage& B = S.ring[slot];
+        if (!w_first) put_w(B);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          B.x[4 * pw + j][0][lane] = xb[j][0];
+          if (p_is_k) B.x[4 * pw + j][1][lane] = xb[j][1];
+        }
+        sup_signal(&S.full[slot]);
+        ++n;
+      }
+      if (!w_first && next_valid) sup_issue_w(a, L, next_t, pw, w);
     }
     prod.next += prod.nwg;
     SupItems::Item pit;
@@ -1282,7 +1310,7 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
   const int g = lane >> 4, col = lane & 15;
   const int hh = wave >> 1, cb = wave & 1;
   const int Sup = a.support;
-  const int nstage = 2 * Sup;
+  const int nstage = 4 * Sup;
   gptr sink = as_global(a.sink) + lane * 512;
   uint32_t n = 0;
   int parity = 0;
@@ -1300,66 +1328,50 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
     auto run = [&](auto is_k_tag) {
       constexpr bool IS_K = decltype(is_k_tag)::value;
       constexpr int XT = IS_K ? 2 : 1;
-      f32x4 acc[4][4];  // [row tile p*2 + q'][column tile]
-      float4 ec[4][2], es[4][2];  // epilogue rotation values, requested two stages ahead
+      f32x4 acc[4][8];  // [row tile p*2 + q'][column tile]
       for (int t = 0; t < nstage; ++t) {
-        const int slot = n & 1;
-        sup_wait(S, &S.full[slot], 4 * ((n >> 1) + 1), a.err);
-        if constexpr (IS_K) {
-          if (t == nstage - 2) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const int tp = S.tpos[parity][(4 * cb + c) * 16 + col];
-#pragma unroll
-              for (int u = 0; u < 2; ++u) {
-                const int64_t off = tab_chunk<16>(tp, 2 * (g & 1) + u, 2 * hh + (g >> 1));
-                ec[c][u] = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
-                es[c][u] = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
-              }
-            }
-          }
-        }
+        const int slot = n % kSupRing;
+        sup_wait(S, &S.full[slot], 4 * (n / kSupRing + 1), a.err);
         const SupStage& B = S.ring[slot];
+        bf16x8 wv[4][2];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          bf16x8 xv[4][XT];
+        for (int rl = 0; rl < 4; ++rl) {
+          const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
+          for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, B.w[rt][tm][lane]);
+        }
 #pragma unroll
-            for (int x = 0; x < XT; ++x) xv[c][x] = __builtin_bit_cast(bf16x8, B.x[4 * cb + c][kk][x][lane]);
-          bf16x8 wv[4][2];
+        for (int c = 0; c < 8; ++c) {
+          bf16x8 xv[XT];
 #pragma unroll
-          for (int rl = 0; rl < 4; ++rl) {
-            const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
-#pragma unroll
-            for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, B.w[rt][kk][tm][lane]);
+          for (int x = 0; x < XT; ++x) xv[x] = __builtin_bit_cast(bf16x8, B.x[8 * cb + c][x][lane]);
+          if (c == 7) {
+            // Every read of this stage is issued: release the buffer once they are done.
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) __hip_atomic_fetch_add(lds_u32(&S.empty[slot]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
           int pi = 0;
           for_products<XT, 2>([&](int ii, int jj) {
 #pragma unroll
-            for (int rl = 0; rl < 4; ++rl)
-#pragma unroll
-              for (int c = 0; c < 4; ++c) {
-                f32x4 cin;
-                if (t == 0 && kk == 0 && pi == 0) {
-                  const float* bp = S.bias[parity] + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
-                  cin = f32x4{bp[0], bp[1], bp[2], bp[3]};
-                } else {
-                  cin = acc[rl][c];
-                }
-                acc[rl][c] = mfma(wv[rl][jj], xv[c][ii], cin);
+            for (int rl = 0; rl < 4; ++rl) {
+              f32x4 cin;
+              if (t == 0 && pi == 0) {
+                const float* bp = S.bias[parity] + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
+                cin = f32x4{bp[0], bp[1], bp[2], bp[3]};
+              } else {
+                cin = acc[rl][c];
               }
+              acc[rl][c] = mfma(wv[rl][jj], xv[ii], cin);
+            }
             ++pi;
           });
         }
-        asm volatile("" ::: "memory");
-        sup_signal(&S.empty[slot]);
         ++n;
       }
       // Epilogue: target RoPE, cast, store.
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int tok = (4 * cb + c) * 16 + col;
+      for (int c = 0; c < 8; ++c) {
+        const int tok = (8 * cb + c) * 16 + col;
         const int row = S.trow[parity][tok];
         float y1[8], y2[8];
 #pragma unroll
@@ -1370,10 +1382,16 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
             y2[4 * q + i] = acc[2 + q][c][i];
           }
         if constexpr (IS_K) {
-          const float cv[8] = {ec[c][0].x, ec[c][0].y, ec[c][0].z, ec[c][0].w,
-                               ec[c][1].x, ec[c][1].y, ec[c][1].z, ec[c][1].w};
-          const float sv[8] = {es[c][0].x, es[c][0].y, es[c][0].z, es[c][0].w,
-                               es[c][1].x, es[c][1].y, es[c][1].z, es[c][1].w};
+          const int tp = S.tpos[parity][tok];
+          float cv[8], sv[8];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int64_t off = tab_chunk<16>(tp, 2 * (g & 1) + u, 2 * hh + (g >> 1));
+            const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
+            const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
+            cv[4 * u] = c4.x; cv[4 * u + 1] = c4.y; cv[4 * u + 2] = c4.z; cv[4 * u + 3] = c4.w;
+            sv[4 * u] = s4.x; sv[4 * u + 1] = s4.y; sv[4 * u + 2] = s4.z; sv[4 * u + 3] = s4.w;
+          }
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float a1 = y1[e], a2 = y2[e];
@@ -1399,11 +1417,11 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
 
 __global__ __launch_bounds__(kSupThreads, 1) void map_install_support_kernel(MapArgs a) {
   __shared__ SupShared S;
-  if (threadIdx.x == 0) {
-    S.full[0] = S.full[1] = 0;
-    S.empty[0] = S.empty[1] = 0;
-    S.abort = 0;
+  if (threadIdx.x < kSupRing) {
+    S.full[threadIdx.x] = 0;
+    S.empty[threadIdx.x] = 0;
   }
+  if (threadIdx.x == 0) S.abort = 0;
   __syncthreads();
   SupItems items;
   items.x = blockIdx.x & 7;

@@ -321,3 +321,48 @@ def test_generic_batch_equals_per_request_installs():
     assert b.mapper.plan.read_errors() == 0
     assert torch.equal(pool.k_data, batched[0]) and torch.equal(pool.v_data, batched[1])
     assert bool(batched[0].abs().sum() > 0)
+
+
+class _LayerPool:
+    """An SGLang-style pool: one K and one V tensor per layer (no shared base),
+    so launches describe it through a device table of per-layer pointers."""
+
+    def __init__(self, pool):
+        self.layer_num, self.start_layer, self.dtype = pool.layer_num, pool.start_layer, pool.dtype
+        self.k_buffer = [b.clone() for b in pool.k_buffer]
+        self.v_buffer = [b.clone() for b in pool.v_buffer]
+
+    def _get_key_buffer(self, layer):
+        return self.k_buffer[layer - self.start_layer]
+
+    def _get_value_buffer(self, layer):
+        return self.v_buffer[layer - self.start_layer]
+
+
+def test_per_layer_pools_on_a_side_stream_match_the_paged_pool():
+    """Per-layer pointer tables stay valid while a launch on another stream
+    reads them, whatever the current stream allocates meanwhile; the rows
+    equal the stride-described pool's bit for bit."""
+    print("per-layer pools on a side stream", flush=True)
+    sh = synthetic.shape("tp4", tokens=512)
+    sh.target_layers = 6
+    h = synthetic.make_handoff(sh, target_pages=64, fill_target="zeros")
+    src, tgt = _LayerPool(h.source_pool), _LayerPool(h.target_pool)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda._sleep(20_000_000)  # keep the side launch queued behind busy work
+    with torch.cuda.stream(side):
+        torch.cuda._sleep(20_000_000)
+    map_install_block(h.mapper, src, h.source_slots, tgt, start=0, stop=512, block_table=h.block_table,
+                      page_size=16, prefix_length=512, stream=side)
+    junk = [torch.full((1 << 18,), -1, dtype=torch.int64, device="cuda") for _ in range(16)]
+    side.synchronize()
+    torch.cuda.synchronize()
+    del junk
+    h.run()
+    torch.cuda.synchronize()
+    assert h.mapper.plan.read_errors() == 0
+    for l in range(sh.target_layers):
+        assert torch.equal(tgt.k_buffer[l], h.target_pool.k_buffer[l])
+        assert torch.equal(tgt.v_buffer[l], h.target_pool.v_buffer[l])
+    assert bool(tgt.k_buffer[0].abs().sum() > 0)
