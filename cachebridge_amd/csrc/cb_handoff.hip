@@ -1333,6 +1333,19 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
         const int slot = n % kSupRing;
         sup_wait(S, &S.full[slot], 4 * (n / kSupRing + 1), a.err);
         const SupStage& B = S.ring[slot];
+        if (t == 0) {
+          // Each row tile's bias is the accumulator input of its first
+          // product (the producers wrote it before the item's first stage).
+          // Set once per item here, so the products below carry no per-MFMA
+          // branch and no wait for the outstanding fragment reads.
+#pragma unroll
+          for (int rl = 0; rl < 4; ++rl) {
+            const float* bp = S.bias[parity] + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
+            const f32x4 b = f32x4{bp[0], bp[1], bp[2], bp[3]};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[rl][c] = b;
+          }
+        }
         bf16x8 wv[4][2];
 #pragma unroll
         for (int rl = 0; rl < 4; ++rl) {
@@ -1340,31 +1353,29 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
 #pragma unroll
           for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, B.w[rt][tm][lane]);
         }
+        // Input fragments flow through a three-slot ring, read two column
+        // tiles ahead of their products; the scheduling barrier keeps the
+        // compiler from sinking each read next to its first use.
+        bf16x8 xv[3][XT];
+        auto read_x = [&](int c, bf16x8 (&dst)[XT]) {
+#pragma unroll
+          for (int x = 0; x < XT; ++x) dst[x] = __builtin_bit_cast(bf16x8, B.x[8 * cb + c][x][lane]);
+        };
+        read_x(0, xv[0]);
+        read_x(1, xv[1]);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          bf16x8 xv[XT];
-#pragma unroll
-          for (int x = 0; x < XT; ++x) xv[x] = __builtin_bit_cast(bf16x8, B.x[8 * cb + c][x][lane]);
+          if (c + 2 < 8) read_x(c + 2, xv[(c + 2) % 3]);
           if (c == 7) {
             // Every read of this stage is issued: release the buffer once they are done.
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (lane == 0) __hip_atomic_fetch_add(lds_u32(&S.empty[slot]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
-          int pi = 0;
           for_products<XT, 2>([&](int ii, int jj) {
 #pragma unroll
-            for (int rl = 0; rl < 4; ++rl) {
-              f32x4 cin;
-              if (t == 0 && pi == 0) {
-                const float* bp = S.bias[parity] + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
-                cin = f32x4{bp[0], bp[1], bp[2], bp[3]};
-              } else {
-                cin = acc[rl][c];
-              }
-              acc[rl][c] = mfma(wv[rl][jj], xv[ii], cin);
-            }
-            ++pi;
+            for (int rl = 0; rl < 4; ++rl) acc[rl][c] = mfma(wv[rl][jj], xv[c % 3][ii], acc[rl][c]);
           });
+          __builtin_amdgcn_sched_barrier(0);
         }
         ++n;
       }
