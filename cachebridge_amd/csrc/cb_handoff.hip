@@ -2421,18 +2421,21 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     }
     if ((rc = upload(&p->d_jobs, jobs.data(), jobs.size() * sizeof(int4), &bytes))) return rc;
   }
-  // Relative cost of one 16-token sub-tile of each unit (streaming kernel):
-  // a per-kind base (gather; keys also un-rotate and read tables) plus a
-  // per-job part (MFMAs, epilogue, stores). A unit that is the only one
-  // reading its source rows fetches all of them from HBM (otherwise another
-  // unit of the group has usually brought them into the MALL first) and runs
-  // ~30% slower per token on MI355X.
+  // Relative cost of one 16-token sub-tile of each unit (streaming kernel),
+  // from per-segment timestamps on MI355X: a two-job key unit 28, a one-job
+  // key unit 21, a two-job value unit 20, a one-job value unit 14 (one job
+  // still pays the whole gather, and keys the un-rotation and tables); keys
+  // with separate rotation tables load them too (+4). A unit that is the only
+  // one reading its source rows fetches all of them from HBM (otherwise
+  // another unit of the group has usually brought them into the MALL first)
+  // and runs ~30% slower per token.
   p->unit_weight.assign(unit_job.size(), 0);
   for (size_t u = 0; u < unit_job.size(); ++u) {
     const int4 m = jobs[unit_job[u]];
     const bool key = (m.y & 0xff) == CB_KIND_K;
-    int w = (key ? 6 : 2) + 4 * unit_njobs[u];
-    if (key && !(m.z & kJobSharedTables)) w += 2;
+    const bool two = unit_njobs[u] == 2;
+    int w = key ? (two ? 28 : 21) : (two ? 20 : 14);
+    if (key && !(m.z & kJobSharedTables)) w += 4;
     if (group_unit_count[unit_group[u]] == 1) w = (w * 13 + 5) / 10;
     p->unit_weight[u] = w;
   }
@@ -2530,7 +2533,7 @@ void class_ranges(const cb_plan* p, int64_t n, int64_t position_start, int64_t p
 // sub-tile weight units: staging the unit's W into LDS, the pipeline ramp and
 // the wait for the slowest wave (tuned on MI355X with the TP4-share and
 // whole-model handoffs).
-constexpr int64_t kSegmentCost = 128;
+constexpr int64_t kSegmentCost = 256;
 
 // Cut the units' sub-tiles, in order, into a.num_blocks contiguous ranges and
 // store the cut points in a.blk_unit / a.blk_sub. A range costs kSegmentCost
