@@ -115,9 +115,14 @@ def _check_pools(h, expected, mapped, tgt_slots):
                        torch.stack([b.cpu()[tgt_slots] for b in h.target_pool.v_buffer])])
     first = [0 if (sh.windows is None or w is None) else max(0, sh.tokens - (w - 1))
              for w in (sh.windows or [None] * sh.target_layers)]
+    # Every kept row of every layer in one comparison: the within-1-ulp share
+    # is a statement about the whole install (a one-token window holds too
+    # few elements for it on its own); the per-element bound applies to all.
+    ot.check_mapped(torch.cat([got[:, l, first[l]:].flatten() for l in range(sh.target_layers)]),
+                    torch.cat([mapped[:, l, first[l]:].flatten() for l in range(sh.target_layers)]),
+                    torch.cat([bound[:, l, first[l]:].flatten() for l in range(sh.target_layers)]))
     for l in range(sh.target_layers):
         f = first[l]
-        ot.check_mapped(got[:, l, f:], mapped[:, l, f:], bound[:, l, f:])
         if f:
             want_untouched = torch.stack([expected.k_buffer[l][tgt_slots[:f]],
                                           expected.v_buffer[l][tgt_slots[:f]]])

@@ -1,0 +1,67 @@
+"""Seeded random model pairs through the fused install, against the oracle.
+
+Each case draws a source and target geometry (layers, heads, selected source
+layers, a random head assignment), head_dim and dtype, a token count that is
+not a multiple of the 16- and 32-token sub-tiles, the page size, per-layer
+target thetas, sliding windows on some layers and a cap on tokens per
+workgroup. The unit structure (one- and two-job units, groups read by a
+single unit, several window classes, segments crossing units) then differs
+from the configured workloads. Rows outside the request and outside each
+layer's window stay bit-identical; mapped rows meet the oracle tolerance
+(module docstring of ``test_gpu_parity``).
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from cachebridge_amd import synthetic
+
+from .test_gpu_parity import _check_pools, _cpu_pool, _oracle_install
+
+pytestmark = pytest.mark.gpu
+
+GEOMETRIES = [(128, torch.bfloat16), (128, torch.bfloat16), (64, torch.bfloat16), (64, torch.float32),
+              (96, torch.bfloat16)]
+
+
+def random_shape(seed: int):
+    """A seeded random handoff shape and tokens-per-workgroup cap."""
+    r = random.Random(seed)
+    d, dtype = r.choice(GEOMETRIES)
+    ls, hs = r.randint(3, 12), r.randint(1, 4)
+    lt, ht = r.randint(2, 9), r.randint(1, 5)
+    selected = sorted(r.sample(range(ls), r.randint(1, min(ls, 6))))
+    windows = None
+    if r.random() < 0.5:  # at most 4 window classes (full history included)
+        windows = [None if r.random() < 0.4 else r.choice([2, 129, 300]) for _ in range(lt)]
+    # Support-s maps (s source pairs per target, head identity) where the
+    # source has the heads and layers for them.
+    support = r.choice([1, 1, 1, 2, 3]) if hs >= ht and ls >= 4 else 1
+    sh = synthetic.Shape(f"random{seed}", ls, hs, lt, ht, d, r.randint(1, 700), dtype, selected,
+                         source_theta=r.choice([1e4, 1e6]),
+                         target_theta=[r.choice([1e4, 1e6]) for _ in range(lt)],
+                         windows=windows, head_map="identity" if support > 1 else "random",
+                         page_size=r.choice([1, 16]), seed=100 + seed, support=support)
+    # The general support-s kernel at D 64 takes caps in 128-token steps.
+    return sh, r.choice([0, 256] if support > 1 else [0, 0, 64, 256])
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_match_oracle(seed):
+    sh, tpw = random_shape(seed)
+    print(f"random shape {seed}: s={sh.support} {sh.source_layers}x{sh.source_heads} -> {sh.target_layers}x"
+          f"{sh.target_heads} D={sh.head_dim} {sh.dtype} T={sh.tokens} page={sh.page_size} "
+          f"windows={sh.windows} tpw={tpw}", flush=True)
+    h = synthetic.make_handoff(sh, fill_target=None)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    for data in (h.target_pool.k_data, h.target_pool.v_data):
+        data.copy_(torch.randn(data.shape, generator=g, device="cuda").to(data.dtype))
+    before = _cpu_pool(h.target_pool)
+    h.run(tokens_per_workgroup=tpw)
+    assert h.mapper.plan.read_errors() == 0
+    mapped, tgt_slots = _oracle_install(h, before)
+    _check_pools(h, before, mapped, tgt_slots)
