@@ -61,7 +61,11 @@ def test_batch_equals_per_request_installs(name, layers, lengths, positions, pre
     pages = sum((n + 15) // 16 for n in lengths) * 2
     h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros")
     spans, bt = _batch(lengths, positions, prefixes, pages, seed=11)
-    bt = bt.to(h.target_pool.device)
+    check_batch_equals_single(h, spans, bt.to(h.target_pool.device))
+
+
+def check_batch_equals_single(h, spans, bt):
+    """One batched launch over ``spans`` against one ``map_install`` per request."""
     map_install_batch(h.mapper, h.source_pool, h.source_slots, h.target_pool, spans,
                       block_table=bt, page_size=16)
     assert h.mapper.plan.read_errors() == 0
@@ -80,11 +84,20 @@ def test_batch_equals_per_request_installs(name, layers, lengths, positions, pre
     assert h.mapper.plan.read_errors() == 0
     assert torch.equal(h.target_pool.k_data, single.k_data)
     assert torch.equal(h.target_pool.v_data, single.v_data)
-    # the batch wrote something in every request's pages (and nothing is all zero by accident)
+    # the batch wrote the last token of every request that some layer keeps
+    # (so the comparison is not between two all-zero pools)
     for sp in spans:
-        if sp.num_tokens:
-            row = int(bt[sp.target_offset // 16]) * 16
+        if sp.num_tokens and _some_layer_keeps_last_token(h.shape, sp):
+            u = sp.target_offset + sp.num_tokens - 1
+            row = int(bt[u // 16]) * 16 + u % 16
             assert h.target_pool.v_data[:, row].abs().sum() > 0
+
+
+def _some_layer_keeps_last_token(sh, sp):
+    """A layer without a window keeps every token; a window W keeps the last W - 1 of the prefix."""
+    prefix = sp.prefix_length or sp.position_start + sp.num_tokens
+    last = sp.position_start + sp.num_tokens - 1
+    return any(w is None or last >= prefix - (w - 1) for w in (sh.windows or [None]))
 
 
 def test_batch_flags_out_of_range_rows_and_skips_them():

@@ -20,6 +20,7 @@ import torch
 
 from cachebridge_amd import synthetic
 
+from .test_gpu_batch import _batch, check_batch_equals_single
 from .test_gpu_parity import _check_pools, _cpu_pool, _oracle_install
 
 pytestmark = pytest.mark.gpu
@@ -65,3 +66,25 @@ def test_random_shapes_match_oracle(seed):
     assert h.mapper.plan.read_errors() == 0
     mapped, tgt_slots = _oracle_install(h, before)
     _check_pools(h, before, mapped, tgt_slots)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batches_equal_per_request_installs(seed):
+    """A random ragged batch (empty requests, offsets into the prefix, prefixes
+    beyond the block) over a random model pair, in one launch, against one
+    launch per request, bit for bit."""
+    sh, _ = random_shape(1000 + seed)
+    sh.page_size = 16
+    r = random.Random(seed)
+    count = r.randint(1, 12)
+    lengths = [r.choice([0, r.randint(1, 40), r.randint(1, 400)]) for _ in range(count)]
+    positions = [r.choice([0, r.randint(0, 500)]) for _ in range(count)]
+    prefixes = [r.choice([0, p + n + r.randint(0, 300)]) for n, p in zip(lengths, positions)]
+    sh.tokens = max(1, sum(lengths))
+    print(f"random batch {seed}: s={sh.support} {sh.source_layers}x{sh.source_heads} -> "
+          f"{sh.target_layers}x{sh.target_heads} D={sh.head_dim} {sh.dtype} windows={sh.windows} "
+          f"lengths={lengths} positions={positions} prefixes={prefixes}", flush=True)
+    pages = sum((n + 15) // 16 for n in lengths) * 2 + 2
+    h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros")
+    spans, bt = _batch(lengths, positions, prefixes, pages, seed=seed)
+    check_batch_equals_single(h, spans, bt.to(h.target_pool.device))
