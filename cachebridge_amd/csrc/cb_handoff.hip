@@ -944,23 +944,24 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
 // for q = 0, 1 and each support member k, k-step q (32 first-half dims)
 // then k-step q + 2 (their RoPE partners).
 //
-// One persistent workgroup of 8 waves per CU, a ring of three stage buffers
-// (W of the k-step: 8 row tiles x 2 terms, 16 KB; the input: 256 tokens x 32
-// dims x 2 terms, 32 KB):
+// One persistent workgroup of 8 waves per CU, a ring of four stage buffers
+// (the input of one k-step: 256 tokens x 32 dims x 2 terms, 32 KB):
 //   - producer waves 4..7 work on k-step pairs {q, q + 2} of one member:
-//     with the pair's W and source dims in registers (requested one pair
-//     ahead), they un-rotate keys and split both halves into bf16 terms,
-//     write the first stage as soon as its buffer is free and signal, hold
-//     the second stage's terms in registers until the next buffer is free,
-//     write and signal it. Producer wave pw holds W fragments of one k-step
-//     and term (k-step slot pw >> 1, term pw & 1) for all 8 row tiles, so
-//     waves 4, 5 write W of the first stage and waves 6, 7 of the second;
-//   - consumer wave (h, c) waits until all four producers have signalled a
-//     stage, multiplies row tiles {h*2 + q', +4} (an output half with its
-//     RoPE partners) by column tiles 8c .. 8c + 7 (128 tokens) into 128
-//     accumulator VGPRs, releases the buffer, and after an item's last
-//     stage runs the epilogue (bias as the first accumulator input, target
-//     RoPE, cast, stores of whole 64-byte chunks of the target rows).
+//     with the pair's source dims in registers (requested one pair ahead),
+//     they un-rotate keys and split both halves into bf16 terms, write the
+//     first stage as soon as its buffer is free and signal, hold the second
+//     stage's terms in registers until the next buffer is free, write and
+//     signal it;
+//   - consumer wave (h, c) loads the W fragments of its row tiles {h*2 + q',
+//     +4} (an output half with its RoPE partners; 2 terms, 8 KB per stage)
+//     straight from memory into registers one stage ahead (the workgroups of
+//     an XCD share each job's W in L2), waits until all four producers have
+//     signalled a stage, multiplies by column tiles 8c .. 8c + 7 (128
+//     tokens) into 128 accumulator VGPRs, releases the buffer, and after an
+//     item's last stage runs the epilogue (bias as the first accumulator
+//     input, target RoPE, cast, stores of whole 64-byte chunks of the target
+//     rows). Keeping W out of the producers shortens their per-pair work,
+//     which bounds the kernel, and leaves LDS room for a fourth stage.
 // Full and empty are monotonic per-buffer counters in LDS (each of the four
 // producer waves adds 1 when its part of a stage is written, each consumer
 // wave adds 1 when its reads of the stage are done), so no workgroup barrier
@@ -984,7 +985,7 @@ constexpr int kSupTile = 256;                 // tokens per item
 constexpr int kSupWaves = 8;                  // 4 consumer and 4 producer waves
 constexpr int kSupThreads = kSupWaves * kWave;
 constexpr int kSupRoleWaves = 4;
-constexpr int kSupRing = 3;
+constexpr int kSupRing = 4;
 
 // Output dim of row r (0..15) of row tile rt (0..7): tile rt = p*4 + h*2 + q
 // holds in lane group g = r / 4 the dims p*64 + h*32 + g*8 + q*4 + r % 4, so
@@ -995,10 +996,8 @@ __host__ __device__ inline int grp_out_dim(int rt, int r) {
   return (rt >> 2) * 64 + ((rt >> 1) & 1) * 32 + (r >> 2) * 8 + (rt & 1) * 4 + (r & 3);
 }
 
-// One stage buffer: W [row tile][term][lane] (16 KB) and the input
-// [column tile][term][lane] (32 KB) of one k-step.
+// One stage buffer: the input [column tile][term][lane] of one k-step (32 KB).
 struct SupStage {
-  uint4 w[8][2][kWave];
   uint4 x[16][2][kWave];
 };
 
@@ -1074,8 +1073,7 @@ __device__ inline void sup_signal(uint32_t* ctr) {
 struct SupLoad {
   bool valid, is_k;
   int npair;            // k-step pairs of the item: 2 * support
-  gcptr wjob;           // the job's packed W, + lane * 16
-  const int32_t* pj;    // the job's support pairs
+  int pjv;              // lane k < support: the job's support pair k
   int kind;
   int64_t soff[4];      // per task: source row byte offset, -1 for the zero row
   int pos[4];           // per task: source position
@@ -1097,8 +1095,12 @@ __device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems
   L.kind = meta_y & 0xff;
   L.is_k = L.kind == CB_KIND_K;
   L.npair = 2 * a.support;
-  L.wjob = as_global(a.w + static_cast<size_t>(it.job) * a.support * Gm<128, uint16_t>::W_U4) + lane * 16;
-  L.pj = a.pairs + static_cast<size_t>(it.job) * a.support;
+  // One vector load per item, waited for with the item's row indices below;
+  // each k-step pair then picks its pair with readlane instead of a scalar
+  // load whose latency would stall every pair.
+  L.pjv = lane < a.support
+              ? reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(a.pairs))[static_cast<size_t>(it.job) * a.support + lane]
+              : 0;
   const int sth = (meta_y >> 16) & 0xff;
   const bool shared = (meta_z & kJobSharedTables) != 0;
   L.ucos = gtab(shared ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
@@ -1126,17 +1128,6 @@ __device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems
   if (pt < D) S.bias[parity][pt] = a.bias[static_cast<size_t>(it.job) * D + pt];
 }
 
-// W of k-step pair t (member k = t % S, q = t / S): the 8 row tiles of
-// k-step slot pw >> 1 (q or q + 2) and term pw & 1.
-__device__ inline void sup_issue_w(const MapArgs& a, const SupLoad& L, int t, int pw, uint4 (&w)[8]) {
-  const int S = a.support;
-  const int q = t >= S ? 1 : 0, k = t - q * S;
-  const int ks = q + 2 * (pw >> 1), tm = pw & 1;
-#pragma unroll
-  for (int rt = 0; rt < 8; ++rt)
-    w[rt] = gload<uint4>(L.wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
-}
-
 // Source dims of k-step pair t for the four tasks: 8 first-half dims and
 // their partners each.
 __device__ inline void sup_issue_x(const MapArgs& a, const SupLoad& L, int t, uint4 (&x)[4][2]) {
@@ -1144,7 +1135,7 @@ __device__ inline void sup_issue_x(const MapArgs& a, const SupLoad& L, int t, ui
   const int S = a.support;
   const int g = (threadIdx.x & (kWave - 1)) >> 4;
   const int q = t >= S ? 1 : 0, k = t - q * S;
-  const int pr = cload(L.pj + k);
+  const int pr = __builtin_amdgcn_readlane(L.pjv, k);
   gcptr base = layer_base(a.src, L.kind, pr & 0xffff) + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * 128 * 2;
   gcptr zrow = as_global(a.zero);
 #pragma unroll
@@ -1184,24 +1175,15 @@ __device__ void sup_producer(const MapArgs& a, SupShared& S, SupItems items) {
   SupLoad L;
   int load_parity = 0;
   sup_decode(a, S, it, 0, pw, L);
-  uint4 w[8], x[4][2];
+  uint4 x[4][2];
   float tc[4][8], ts[4][8];
-  sup_issue_w(a, L, 0, pw, w);
   if (L.is_k) sup_issue_tab(L, 0, tc, ts);
   sup_issue_x(a, L, 0, x);
   int lt = 1;       // pair of L the next loads are for
   uint32_t n = 0;   // global stage index
   bool p_is_k = L.is_k;
-  const bool w_first = pw < 2;  // this wave's W fragments belong to the pair's first stage
 
-  auto put_w = [&](SupStage& B) {
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) B.w[rt][pw & 1][lane] = w[rt];
-  };
-
-  // Requests the next pair's loads (advancing L at its end); ``part`` 0
-  // requests the source dims (and W when this wave's W went out with the
-  // first stage), part 1 the rest of W.
+  // Moves the loads to the next pair (and L to the next item at its end).
   bool next_valid = true;
   int next_t = 0;
   auto advance = [&]() {
@@ -1267,7 +1249,6 @@ __device__ void sup_producer(const MapArgs& a, SupShared& S, SupItems items) {
         const int slot = n % kSupRing;
         sup_wait(S, &S.empty[slot], 4 * (n / kSupRing), a.err);
         SupStage& B = S.ring[slot];
-        if (w_first) put_w(B);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           B.x[4 * pw + j][0][lane] = xa[j][0];
@@ -1276,13 +1257,11 @@ __device__ void sup_producer(const MapArgs& a, SupShared& S, SupItems items) {
         sup_signal(&S.full[slot]);
         ++n;
       }
-      if (w_first && next_valid) sup_issue_w(a, L, next_t, pw, w);
       // Second stage (k-step q + 2).
       {
         const int slot = n % kSupRing;
         sup_wait(S, &S.empty[slot], 4 * (n / kSupRing), a.err);
         SupStage& B = S.ring[slot];
-        if (!w_first) put_w(B);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           B.x[4 * pw + j][0][lane] = xb[j][0];
@@ -1291,7 +1270,6 @@ __device__ void sup_producer(const MapArgs& a, SupShared& S, SupItems items) {
         sup_signal(&S.full[slot]);
         ++n;
       }
-      if (!w_first && next_valid) sup_issue_w(a, L, next_t, pw, w);
     }
     prod.next += prod.nwg;
     SupItems::Item pit;
@@ -1325,11 +1303,30 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
     const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
     const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
 
+    // The job's packed W [member][row tile][k-step][term][lane]: this wave's
+    // fragments of stage t (member k, k-step ks; stages are k-step pairs
+    // {q, q + 2} of each member, q = 0 then 1) for row tiles
+    // (rl >> 1) * 4 + hh * 2 + (rl & 1).
+    gcptr wjob = as_global(a.w + static_cast<size_t>(it.job) * Sup * Gm<128, uint16_t>::W_U4) + lane * 16;
+    auto issue_w = [&](int t, uint4 (&dst)[4][2]) __attribute__((always_inline)) {
+      const int p = t >> 1, q = p >= Sup ? 1 : 0, k = p - q * Sup, ks = q + 2 * (t & 1);
+#pragma unroll
+      for (int rl = 0; rl < 4; ++rl) {
+        const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm)
+          dst[rl][tm] = gload<uint4>(wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
+      }
+    };
+
     auto run = [&](auto is_k_tag) {
       constexpr bool IS_K = decltype(is_k_tag)::value;
       constexpr int XT = IS_K ? 2 : 1;
       f32x4 acc[4][8];  // [row tile p*2 + q'][column tile]
-      for (int t = 0; t < nstage; ++t) {
+      uint4 wr[2][4][2];  // W fragments of the current stage and the next
+      issue_w(0, wr[0]);
+      auto stage = [&](int t, const uint4 (&cur)[4][2], uint4 (&nxt)[4][2]) __attribute__((always_inline)) {
+        if (t + 1 < nstage) issue_w(t + 1, nxt);
         const int slot = n % kSupRing;
         sup_wait(S, &S.full[slot], 4 * (n / kSupRing + 1), a.err);
         const SupStage& B = S.ring[slot];
@@ -1348,11 +1345,9 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
         }
         bf16x8 wv[4][2];
 #pragma unroll
-        for (int rl = 0; rl < 4; ++rl) {
-          const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
+        for (int rl = 0; rl < 4; ++rl)
 #pragma unroll
-          for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, B.w[rt][tm][lane]);
-        }
+          for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, cur[rl][tm]);
         // Input fragments flow through a three-slot ring, read two column
         // tiles ahead of their products; the scheduling barrier keeps the
         // compiler from sinking each read next to its first use.
@@ -1378,6 +1373,12 @@ __device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
           __builtin_amdgcn_sched_barrier(0);
         }
         ++n;
+      };
+      // Two stages per step, so the W register slots are compile-time
+      // constants (a runtime-indexed register array would live in scratch).
+      for (int t = 0; t < nstage; t += 2) {
+        stage(t, wr[0], wr[1]);
+        stage(t + 1, wr[1], wr[0]);
       }
       // Epilogue: target RoPE, cast, store.
 #pragma unroll
