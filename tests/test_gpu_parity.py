@@ -198,15 +198,16 @@ def test_out_of_range_slots_are_flagged_not_written():
     assert flags & 1
 
 
-@pytest.mark.parametrize("dim,dtype,support", [(64, torch.bfloat16, 3), (64, torch.float32, 2),
-                                               (128, torch.bfloat16, 3)])
-def test_support_maps_match_oracle(dim, dtype, support):
+@pytest.mark.parametrize("dim,dtype,support,n", [(64, torch.bfloat16, 3, 200), (64, torch.float32, 2, 200),
+                                                 (128, torch.bfloat16, 3, 200), (128, torch.bfloat16, 16, 600)])
+def test_support_maps_match_oracle(dim, dtype, support, n):
     """Support-s maps at every kernel that takes them: the general kernel (D 64
-    bf16 and fp32 I/O) and the blocked support kernel (D 128 bf16, s = 3; a block
-    of 200 tokens is one full and one partial 128-token block)."""
-    print(f"support maps D={dim} {dtype} s={support}", flush=True)
+    bf16 and fp32 I/O) and the support kernel (D 128 bf16: s = 3 over one
+    partial 256-token item, and the largest support, s = 16, over two full
+    items and a partial one)."""
+    print(f"support maps D={dim} {dtype} s={support} n={n}", flush=True)
     g = torch.Generator().manual_seed(11 + dim + support)
-    ls, hs, lt, ht, n, p0 = 6, 2, 3, 2, 200, 300
+    ls, hs, lt, ht, p0 = max(6, support), 2, 3, 2, 300
     layers = torch.stack([torch.randperm(ls, generator=g)[:support] for _ in range(lt * ht)])
     spec = {"assign_layer": layers.view(lt, ht, support),
             "assign_head": torch.randint(0, hs, (lt, ht, support), generator=g),
@@ -226,7 +227,7 @@ def test_support_maps_match_oracle(dim, dtype, support):
 
 
 def test_support_items_ignore_tokens_per_workgroup():
-    """The support kernel's items are fixed 128-token blocks: a launch with a
+    """The support kernel's items are fixed 256-token blocks: a launch with a
     larger tokens_per_workgroup writes every token, bit-identically."""
     print("support s8 tokens_per_workgroup", flush=True)
     sh = synthetic.shape("tp4_s8", tokens=600)
