@@ -2510,7 +2510,10 @@ int check_sides(const cb_plan* p, const cb_rows& sr, const cb_rows& tr) {
   if (tr.index_kind == CB_INDEX_IDENTITY && sr.index_kind == CB_INDEX_IDENTITY &&
       tr.k_base == sr.k_base && tr.k_base)
     return fail(CB_EINVAL, "target aliases the source");
-  if (p->info.support == 1 && (sr.rows > INT32_MAX || tr.rows > INT32_MAX))
+  // The streaming and support kernels keep row indices in 32 bits; the
+  // generic kernels take 64-bit rows.
+  const bool rows32 = !p->generic && (p->info.support == 1 || p->support_gemm);
+  if (rows32 && (sr.rows > INT32_MAX || tr.rows > INT32_MAX))
     return fail(CB_EINVAL, "pools with more than 2^31 rows are not supported");
   return CB_OK;
 }

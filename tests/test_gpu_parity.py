@@ -226,6 +226,38 @@ def test_support_maps_match_oracle(dim, dtype, support, n):
     print(ot.check_mapped(out, ref, bound, abs_factor=_factor(dtype)), flush=True)
 
 
+@pytest.mark.parametrize("support", [1, 2])
+def test_pools_beyond_int32_rows_are_rejected_before_launch(support):
+    """The streaming (s = 1) and support (s > 1) kernels keep row indices in 32
+    bits, so a pool described with more than 2^31 rows is refused on the host
+    and nothing is written. (The descriptions cover real, small buffers and the
+    identity index only reaches their first rows, so the call would stay in
+    bounds even without the check.)"""
+    from cachebridge_amd import plan as cplan
+    print(f"int32 row guard s={support}", flush=True)
+    g = torch.Generator().manual_seed(5 + support)
+    ls, hs, lt, ht, n, d = 4, 2, 2, 2, 64, 128
+    spec = {"assign_layer": torch.stack([torch.randperm(ls, generator=g)[:support] for _ in range(lt * ht)]).view(lt, ht, support),
+            "assign_head": torch.randint(0, hs, (lt, ht, support), generator=g),
+            "k_weight": torch.randn(lt, ht, support * d, d, generator=g) / (support * d) ** 0.5,
+            "v_weight": torch.randn(lt, ht, support * d, d, generator=g) / (support * d) ** 0.5,
+            "k_bias": torch.zeros(lt, ht, d), "v_bias": torch.zeros(lt, ht, d)}
+    mapper = HeadwiseMapper.from_assignment(**spec, source_rope_theta=1e4, target_rope_theta=1e4,
+                                            dtype=torch.bfloat16, device="cuda", max_positions=256)
+    page = torch.randn(2, ls, n, hs, d, generator=g).to(torch.bfloat16).cuda()
+    out = torch.zeros(2, lt, n, ht, d, dtype=torch.bfloat16, device="cuda")
+    for side in ("source", "target"):
+        src, tgt = cplan.rows_from_page(page), cplan.rows_from_page(out)
+        (src if side == "source" else tgt).c.rows = 2 ** 31 + 1
+        with pytest.raises(ValueError, match="2\\^31"):
+            mapper.plan.launch(src, tgt, num_tokens=n, position_start=0)
+    torch.cuda.synchronize()
+    assert not out.any()
+    mapper.plan.launch(cplan.rows_from_page(page), cplan.rows_from_page(out), num_tokens=n, position_start=0)
+    torch.cuda.synchronize()
+    assert out.any()
+
+
 def test_support_items_ignore_tokens_per_workgroup():
     """The support kernel's items are fixed 256-token blocks: a launch with a
     larger tokens_per_workgroup writes every token, bit-identically."""
