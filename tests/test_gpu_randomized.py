@@ -51,7 +51,7 @@ def random_shape(seed: int):
     return sh, r.choice([0, 256] if support > 1 else [0, 0, 64, 256])
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_random_shapes_match_oracle(seed):
     sh, tpw = random_shape(seed)
     print(f"random shape {seed}: s={sh.support} {sh.source_layers}x{sh.source_heads} -> {sh.target_layers}x"
@@ -68,7 +68,7 @@ def test_random_shapes_match_oracle(seed):
     _check_pools(h, before, mapped, tgt_slots)
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_batches_equal_per_request_installs(seed):
     """A random ragged batch (empty requests, offsets into the prefix, prefixes
     beyond the block) over a random model pair, in one launch, against one
