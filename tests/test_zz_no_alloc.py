@@ -40,19 +40,22 @@ def _zero_pool_like(pool):
                        device=pool.device, fill="zeros")
 
 
-def test_noalloc_batch_equals_allocating_batch_on_two_calls():
+@pytest.mark.parametrize("workload", ["tp4", "tp4_s8"])
+def test_noalloc_batch_equals_allocating_batch_on_two_calls(workload):
+    """Both map kernels a batch can use: the streaming kernel (support 1) and
+    the support kernel (support 8)."""
     lib = _lib.load()
     batches = [([700, 1, 300, 1500, 17, 900, 64], [0, 5, 0, 40, 0, 100, 7]),
                ([200, 33], [0, 3])]
     tokens = sum(batches[0][0])
-    sh = synthetic.shape("tp4", tokens=tokens)
+    sh = synthetic.shape(workload, tokens=tokens)
     sh.target_layers = 6
     pages = sum((n + 15) // 16 for n in batches[0][0]) * 2
     h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros")
     plan = h.mapper.plan
     stream = torch.cuda.current_stream()
     for call, (lengths, positions) in enumerate(batches):
-        print(f"no-alloc call {call}: {len(lengths)} requests, {sum(lengths)} tokens", flush=True)
+        print(f"no-alloc {workload} call {call}: {len(lengths)} requests, {sum(lengths)} tokens", flush=True)
         spans, bt = _spans(lengths, positions, pages, seed=20 + call)
         bt = bt.to(h.target_pool.device)
         want, got = _zero_pool_like(h.target_pool), _zero_pool_like(h.target_pool)
