@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -365,6 +366,15 @@ struct MapArgs {
   // rows: src/tgt are int32 row vectors over the same token space). Null for
   // one request, whose token t sits at position_start + t.
   const int32_t* pos;
+  // Streaming kernel work pool: after its own range, each workgroup claims
+  // chunks of the cost line's tail [(pool_u0, pool_s0), end) until pool_n are
+  // taken (pool_n 0: no pool). Chunks hold pool_gs sub-tiles (fewer at a
+  // unit's end) and never span two units.
+  uint32_t* pool_ctr;  // this launch's (claims, finished workgroups)
+  int32_t pool_n;
+  int32_t pool_u0;
+  int32_t pool_s0;
+  int32_t pool_gs;
 };
 
 // Job flag (meta.z): un-rotation uses the rotation table (same theta, unit norm).
@@ -417,6 +427,42 @@ __host__ __device__ inline int class_of_unit(const MapArgs& a, int u) {
   int c = 0;
   while (c + 1 < a.ncls && u >= a.cls_unit_end[c]) ++c;
   return c;
+}
+
+// Work-pool chunk idx -> (unit, first sub-tile), or false past the pool. The
+// tail from (pool_u0, pool_s0) is cut unit by unit into chunks of pool_gs
+// sub-tiles (the first unit's from pool_s0); every unit of a window class has
+// the same sub-tiles, so a class's chunks are counted in closed form from the
+// kernel arguments alone (no memory loads).
+__host__ __device__ inline bool pool_chunk(const MapArgs& a, int64_t idx, int* unit, int* sub) {
+  const int gs = a.pool_gs;
+  int u = a.pool_u0;
+  int c = class_of_unit(a, u);
+  {
+    const int ns = a.cls_subtiles[c];
+    const int64_t first = ns > a.pool_s0 ? (ns - a.pool_s0 + gs - 1) / gs : 0;
+    if (idx < first) {
+      *unit = u;
+      *sub = a.pool_s0 + static_cast<int>(idx) * gs;
+      return true;
+    }
+    idx -= first;
+    ++u;
+  }
+  for (; c < a.ncls && u < a.num_units; ++c) {
+    const int cend = c + 1 < a.ncls ? a.cls_unit_end[c] : a.num_units;
+    if (u >= cend) continue;
+    const int64_t per = (a.cls_subtiles[c] + gs - 1) / gs;
+    const int64_t n = static_cast<int64_t>(cend - u) * per;
+    if (idx < n) {
+      *unit = u + static_cast<int>(idx / per);
+      *sub = static_cast<int>(idx % per) * gs;
+      return true;
+    }
+    idx -= n;
+    u = cend;
+  }
+  return false;
 }
 
 // MFMA product schedule: term pairs (i of x, j of w) with i + j < NTW, small first.
@@ -899,19 +945,20 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
   __shared__ uint4 lds_w[kUnitJobs * Gm<D, IO>::W_U4];
   __shared__ float lds_bias[kUnitJobs * D];
   __shared__ int lds_next;  // next sub-tile to claim in the current segment
+  __shared__ int lds_chunk;  // work-pool chunk claimed by the workgroup
   const int per = a.num_blocks >> 3;
   const int r = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
   Pos cur{a.blk_unit[r], a.blk_sub[r]};
   const Pos end{a.blk_unit[r + 1], a.blk_sub[r + 1]};
-  while (cur.unit < end.unit || (cur.unit == end.unit && cur.sub < end.sub)) {
-    const int c = class_of_unit(a, cur.unit);
-    const int stop = cur.unit == end.unit ? end.sub : a.cls_subtiles[c];
-    if (stop > cur.sub) {
+  // One segment: sub-tiles [sub0, stop) of unit u_in (stop > sub0).
+  auto seg = [&](int u_in, int sub0, int stop) __attribute__((always_inline)) {
+    const int c = class_of_unit(a, u_in);
+    {
       Work wk;
-      const int unit = __builtin_amdgcn_readfirstlane(cur.unit);  // wave-uniform: scalar loads
+      const int unit = __builtin_amdgcn_readfirstlane(u_in);  // wave-uniform: scalar loads
       wk.job = __builtin_amdgcn_readfirstlane(cload(a.unit_job + unit));
       wk.njobs = cload(a.unit_njobs + unit);
-      wk.tok_lo = a.cls_tok_first[c] + cur.sub * kSubTokens;
+      wk.tok_lo = a.cls_tok_first[c] + sub0 * kSubTokens;
       wk.tok_hi = min(a.cls_tok_first[c] + stop * kSubTokens, a.cls_tok_first[c] + a.cls_tok_count[c]);
       const int* mp = reinterpret_cast<const int*>(a.jobs + wk.job);
       const int meta_y = cload(mp + 1), meta_z = cload(mp + 2);
@@ -929,7 +976,40 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
         else stream_run<D, IO, false, false, 1, 2, POS>(a, lds_w, lds_bias, &lds_next, wk);
       }
     }
+  };
+  while (cur.unit < end.unit || (cur.unit == end.unit && cur.sub < end.sub)) {
+    const int c = class_of_unit(a, cur.unit);
+    const int stop = cur.unit == end.unit ? end.sub : a.cls_subtiles[c];
+    if (stop > cur.sub) seg(cur.unit, cur.sub, stop);
     cur = Pos{cur.unit + 1, 0};
+  }
+  if (a.pool_n <= 0) return;
+  // Work pool: a workgroup done with its own range claims chunks of the
+  // line's tail in order until all pool_n are taken. (The segment body is
+  // instantiated twice: one loop for both kinds of segments made the compiler
+  // reserve a private segment.)
+  for (;;) {
+    __syncthreads();  // every wave has read the previous claim
+    if (threadIdx.x == 0) lds_chunk = static_cast<int>(atomicAdd(a.pool_ctr, 1u));
+    __syncthreads();
+    const int idx = __builtin_amdgcn_readfirstlane(lds_chunk);
+    if (idx >= a.pool_n) break;
+    int pu = 0, ps = 0;
+    if (!pool_chunk(a, idx, &pu, &ps)) {  // pool_n exceeds the tail's chunks: a host-side bug
+      if (threadIdx.x == 0) atomicOr(a.err, 4);
+      break;
+    }
+    seg(pu, ps, min(a.cls_subtiles[class_of_unit(a, pu)], ps + a.pool_gs));
+  }
+  // The last workgroup to finish clears the launch's counter pair (every
+  // claim of the launch has been made by then), so the next launch on this
+  // pair starts from zero without a host-side clear.
+  if (threadIdx.x == 0) {
+    const uint32_t done = atomicAdd(a.pool_ctr + 1, 1u);
+    if (done == gridDim.x - 1) {
+      atomicExch(a.pool_ctr, 0u);
+      atomicExch(a.pool_ctr + 1, 0u);
+    }
   }
 }
 
@@ -2207,6 +2287,8 @@ static_assert(3 * ((int64_t{CB_NOALLOC_MAX_TOKENS} * 4 + 255) / 256 * 256) <= CB
 // Host side
 // ---------------------------------------------------------------------------
 
+constexpr int kPoolSlots = 64;  // work-pool counter pairs per plan
+
 struct cb_plan {
   int device = 0;
   cb_plan_info info{};
@@ -2236,6 +2318,11 @@ struct cb_plan {
   // each window class), reused by launches with the same shape.
   mutable std::mutex split_mu;
   mutable std::vector<int32_t> split_key, split_unit, split_sub;
+  mutable int32_t split_pool[4] = {0, 0, 0, 0};  // pool_n, pool_u0, pool_s0, pool_gs
+  // Work-pool counters of the streaming kernel: kPoolSlots pairs (claims,
+  // finished workgroups), zero between launches; launch k uses pair k % kPoolSlots.
+  uint32_t* d_pool = nullptr;
+  mutable std::atomic<uint32_t> pool_seq{0};
   float* d_cos = nullptr;
   float* d_sin = nullptr;
   float* d_ucos = nullptr;
@@ -2251,7 +2338,8 @@ void plan_free(cb_plan* p) {
   void* ptrs[] = {p->d_w,         p->d_bias,         p->d_jobs,           p->d_pairs,
                   p->d_unit_job,  p->d_unit_njobs,   p->d_unit_group,     p->d_group_unit_start,
                   p->d_group_unit_count, p->d_cos,   p->d_sin,            p->d_ucos,
-                  p->d_usin,      p->d_err,          p->d_sink};
+                  p->d_usin,      p->d_err,          p->d_sink,
+                  p->d_pool};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
   delete p;
@@ -2440,6 +2528,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     if (group_unit_count[unit_group[u]] == 1) w = (w * 13 + 5) / 10;
     p->unit_weight[u] = w;
   }
+  if ((rc = upload(&p->d_pool, nullptr, 2 * kPoolSlots * sizeof(uint32_t), &bytes))) return rc;
+  CB_HIP(hipMemset(p->d_pool, 0, 2 * kPoolSlots * sizeof(uint32_t)));
   int32_t* d_order = nullptr;
   CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), order.size() * 4));
   hipError_t e = hipMemcpy(d_order, order.data(), order.size() * 4, hipMemcpyHostToDevice);
@@ -2539,11 +2629,40 @@ void class_ranges(const cb_plan* p, int64_t n, int64_t position_start, int64_t p
 // whole-model handoffs).
 constexpr int64_t kSegmentCost = 256;
 
+// Work pool of the streaming kernel. Workgroups drift apart over a long
+// launch (memory contention differs between XCDs and over time), so when a
+// workgroup's share of the cost line is long the line's tail is not cut into
+// static ranges but handed out in chunks to whichever workgroup is free.
+// Every chunk pays a segment start, so short launches keep static ranges
+// only. Per-workgroup budgets are in sub-tile weight units (the TP4-share
+// 4096-token handoff: about 3.2K; the whole 64x8 model: 13K; the 32K-token
+// history and the 64-request batch: about 100K). Measured on MI355X.
+#ifndef CB_POOL_MID_BUDGET
+#define CB_POOL_MID_BUDGET 8192   // below: no pool
+#endif
+#ifndef CB_POOL_LONG_BUDGET
+#define CB_POOL_LONG_BUDGET 32768
+#endif
+#ifndef CB_POOL_MID_PCT           // share of the line in the pool, chunk cost (% of a budget)
+#define CB_POOL_MID_PCT 15
+#endif
+#ifndef CB_POOL_MID_CHUNK_PCT
+#define CB_POOL_MID_CHUNK_PCT 8
+#endif
+#ifndef CB_POOL_LONG_PCT
+#define CB_POOL_LONG_PCT 25
+#endif
+#ifndef CB_POOL_LONG_CHUNK_PCT
+#define CB_POOL_LONG_CHUNK_PCT 5
+#endif
+
 // Cut the units' sub-tiles, in order, into a.num_blocks contiguous ranges and
 // store the cut points in a.blk_unit / a.blk_sub. A range costs kSegmentCost
 // per unit it touches plus its sub-tiles' weights; the cuts minimise the
 // largest range cost (greedy fill for a given budget, bisection on the
-// budget), so ranges that cross a unit boundary get fewer sub-tiles.
+// budget), so ranges that cross a unit boundary get fewer sub-tiles. With a
+// work pool, the ranges are filled to a smaller budget and the rest of the
+// line becomes the pool (a->pool_*).
 void split_cost_line(const cb_plan* p, MapArgs* a) {
   const int nu = p->num_units, nb = a->num_blocks;
   std::vector<int32_t> ns(nu, 0);
@@ -2555,11 +2674,16 @@ void split_cost_line(const cb_plan* p, MapArgs* a) {
     if (ns[u] > 0) total += kSegmentCost + static_cast<int64_t>(p->unit_weight[u]) * ns[u];
   }
   // Greedy fill with budget T per range; returns the ranges used (cuts into
-  // blk_* when `out`).
+  // blk_* when `out`). With `out`, at most nb ranges are cut and the rest of
+  // the line, from (u, sub), is left to the pool; cuts past the last range
+  // all sit at that point.
+  int u = 0, sub = 0;
   auto fill = [&](int64_t T, bool out) {
-    int u = 0, sub = 0, r = 0;
+    u = 0;
+    sub = 0;
+    int r = 0;
     while (u < nu && ns[u] == 0) ++u;
-    while (u < nu) {
+    while (u < nu && !(out && r == nb)) {
       if (out) {
         a->blk_unit[r] = u;
         a->blk_sub[r] = sub;
@@ -2586,8 +2710,8 @@ void split_cost_line(const cb_plan* p, MapArgs* a) {
     }
     if (out) {
       for (int q = r; q <= nb; ++q) {
-        a->blk_unit[q] = nu;
-        a->blk_sub[q] = 0;
+        a->blk_unit[q] = u;
+        a->blk_sub[q] = sub;
       }
     }
     return r;
@@ -2598,7 +2722,48 @@ void split_cost_line(const cb_plan* p, MapArgs* a) {
     if (fill(mid, false) <= nb) hi = mid;
     else lo = mid + 1;
   }
-  fill(lo, true);
+  int64_t pool_pct = 0, chunk_pct = 0;
+  if (lo >= CB_POOL_LONG_BUDGET) {
+    pool_pct = CB_POOL_LONG_PCT;
+    chunk_pct = CB_POOL_LONG_CHUNK_PCT;
+  } else if (lo >= CB_POOL_MID_BUDGET) {
+    pool_pct = CB_POOL_MID_PCT;
+    chunk_pct = CB_POOL_MID_CHUNK_PCT;
+  }
+  a->pool_n = 0;
+  a->pool_u0 = nu;
+  a->pool_s0 = 0;
+  a->pool_gs = 1;
+  if (pool_pct <= 0) {
+    fill(lo, true);
+    return;
+  }
+  fill(lo * (100 - pool_pct) / 100, true);  // leaves (u, sub) at the pool's start
+  // Chunks of about chunk_pct% of a budget: sub-tiles at the pool's mean
+  // sub-tile weight, at least 4.
+  int64_t pool_w = 0, pool_subs = 0;
+  for (int v = u; v < nu; ++v) {
+    const int s0 = v == u ? sub : 0;
+    if (ns[v] > s0) {
+      pool_w += static_cast<int64_t>(p->unit_weight[v]) * (ns[v] - s0);
+      pool_subs += ns[v] - s0;
+    }
+  }
+  if (pool_subs == 0) return;  // the ranges reach the line's end
+  const int64_t gs = std::max<int64_t>(4, lo * chunk_pct / 100 * pool_subs / pool_w);
+  int64_t chunks = 0;
+  for (int v = u; v < nu; ++v) {
+    const int s0 = v == u ? sub : 0;
+    if (ns[v] > s0) chunks += (ns[v] - s0 + gs - 1) / gs;
+  }
+  if (chunks > (int64_t{1} << 24) || gs > INT32_MAX) {  // not a useful pool: static ranges only
+    fill(lo, true);
+    return;
+  }
+  a->pool_n = static_cast<int32_t>(chunks);
+  a->pool_u0 = u;
+  a->pool_s0 = sub;
+  a->pool_gs = static_cast<int32_t>(gs);
 }
 
 // Enqueue the map kernel over class token ranges [first[c], first[c] +
@@ -2678,12 +2843,21 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
     if (key == p->split_key) {
       std::copy(p->split_unit.begin(), p->split_unit.end(), a.blk_unit);
       std::copy(p->split_sub.begin(), p->split_sub.end(), a.blk_sub);
+      a.pool_n = p->split_pool[0];
+      a.pool_u0 = p->split_pool[1];
+      a.pool_s0 = p->split_pool[2];
+      a.pool_gs = p->split_pool[3];
     } else {
       split_cost_line(p, &a);
       p->split_key = key;
       p->split_unit.assign(a.blk_unit, a.blk_unit + nbk);
       p->split_sub.assign(a.blk_sub, a.blk_sub + nbk);
+      p->split_pool[0] = a.pool_n;
+      p->split_pool[1] = a.pool_u0;
+      p->split_pool[2] = a.pool_s0;
+      p->split_pool[3] = a.pool_gs;
     }
+    a.pool_ctr = p->d_pool + 2 * (p->pool_seq.fetch_add(1, std::memory_order_relaxed) % kPoolSlots);
   }
   const dim3 grid(static_cast<unsigned>(grid_blocks)), block(ws ? kStreamThreads : kThreads);
   if (ws) {

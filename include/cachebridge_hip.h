@@ -260,7 +260,9 @@ int cb_delta_state_transform(int32_t dtype, int64_t batch, int32_t k, int32_t v,
                              void* d_out, int64_t out_stride, void* stream);
 
 /* Read and clear the plan's device error word (bit 0: source row out of
-   range, bit 1: target row out of range). Synchronizes `stream`. */
+   range, bit 1: target row out of range, bit 2: a kernel's internal schedule
+   failed -- a bounded wait of the support kernel timed out, or a work-pool
+   claim of the streaming kernel fell past its pool). Synchronizes `stream`. */
 int cb_plan_read_errors(cb_plan* plan, int32_t* flags, void* stream);
 
 #ifdef __cplusplus

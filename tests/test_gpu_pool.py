@@ -1,0 +1,75 @@
+"""GPU: the streaming kernel's work pool.
+
+When a workgroup's share of a launch is long, the streaming kernel leaves the
+tail of its work line to a pool of chunks that free workgroups claim from a
+counter pair in plan-owned device memory; the launch's last workgroup clears
+the pair, and a plan rotates over 64 pairs. The whole 40x8 -> 64x8 model at
+4096 tokens is such a launch (about 13K weight units of work per workgroup,
+above the pool threshold of 8192); 512-token launches of the same work are
+not (below 2K). These tests check that every launch of a pooled shape
+installs every row, across more launches than the plan has counter pairs and
+with launches overlapping on two streams.
+"""
+
+from __future__ import annotations
+
+import gc
+
+import pytest
+import torch
+
+from cachebridge_amd import synthetic
+from tests import fullsize as fs
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _release_memory():
+    yield
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def test_pool_installs_every_row_over_many_launches():
+    sh = synthetic.shape("full")
+    n = sh.tokens
+    print(f"pooled handoff: {sh.source_layers}x{sh.source_heads} -> {sh.target_layers}x{sh.target_heads}, "
+          f"{n} tokens, 512 target pages", flush=True)
+    h = synthetic.make_handoff(sh, target_pages=512, device_source=True)
+    pool = h.target_pool
+    slots = synthetic.slots_from_pages(h.block_table.cpu(), n, sh.page_size).to(pool.k_data.device)
+    written = [slots] * sh.target_layers
+
+    fs.fill_sentinel(pool)
+    h.run()
+    assert h.mapper.plan.read_errors() == 0
+    fs.check_untouched(pool, written)
+    ref = fs.snapshot(pool, slots)
+
+    # Launches overlapping on two streams take different counter pairs.
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for _ in range(8):
+        h.run(stream=s1)
+        h.run(stream=s2)
+    torch.cuda.synchronize()
+    assert torch.equal(fs.snapshot(pool, slots), ref)
+
+    # Every counter pair then serves two more launches; each must install
+    # every row (a pair left non-zero would make its next launch skip chunks,
+    # leaving sentinel rows).
+    for i in range(2 * 64 + 3):
+        fs.fill_sentinel(pool)
+        h.run()
+        assert torch.equal(fs.snapshot(pool, slots), ref), f"launch {i} after the overlapping ones"
+    assert h.mapper.plan.read_errors() == 0
+
+    # 512-token launches (no pool) write the same rows bit for bit.
+    fs.fill_sentinel(pool)
+    for start in range(0, n, 512):
+        h.run(start=start, stop=min(n, start + 512))
+    assert h.mapper.plan.read_errors() == 0
+    assert torch.equal(fs.snapshot(pool, slots), ref)
+    fs.check_untouched(pool, written)
