@@ -4,8 +4,10 @@
 batches in a row, the second smaller than the first (so stale workspace
 contents from the first call would show), and each result is compared bit for
 bit with ``cb_map_install_batch`` given a torch-allocated workspace (that path
-is pinned against the oracle by the batch and full-size tests). A batch beyond
-the fixed workspace is rejected before anything is enqueued.
+is pinned against the oracle by the batch and full-size tests). A batch long
+enough for the streaming kernel's work pool runs the same way, twice around a
+short one. A batch beyond the fixed workspace is rejected before anything is
+enqueued.
 """
 
 from __future__ import annotations
@@ -71,6 +73,42 @@ def test_noalloc_batch_equals_allocating_batch_on_two_calls(workload):
         assert torch.equal(got.k_data, want.k_data)
         assert torch.equal(got.v_data, want.v_data)
         assert int(got.v_data.abs().sum()) > 0
+
+
+def test_noalloc_pooled_batch_equals_allocating_batch():
+    """A batch long enough for the streaming kernel's work pool (5,100 tokens
+    into the whole 40x8 -> 64x8 model: about 16K weight units per workgroup,
+    above the pool threshold of 8,192), then a short one without the pool,
+    then the long one again: the pool's claim counters live in plan-owned
+    device memory and are cleared by each launch's last workgroup, so the
+    no-allocation call needs nothing more."""
+    lib = _lib.load()
+    batches = [([1500, 2000, 900, 700], [0, 0, 64, 3]), ([300, 1200], [0, 9]),
+               ([1500, 2000, 900, 700], [0, 0, 64, 3])]
+    tokens = sum(batches[0][0])
+    sh = synthetic.shape("full", tokens=tokens)
+    pages = sum((n + 15) // 16 for n in batches[0][0]) * 2
+    h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros", device_source=True)
+    plan = h.mapper.plan
+    stream = torch.cuda.current_stream()
+    for call, (lengths, positions) in enumerate(batches):
+        print(f"no-alloc pooled call {call}: {len(lengths)} requests, {sum(lengths)} tokens", flush=True)
+        spans, bt = _spans(lengths, positions, pages, seed=40 + call)
+        bt = bt.to(h.target_pool.device)
+        want, got = _zero_pool_like(h.target_pool), _zero_pool_like(h.target_pool)
+        src = pool_rows(h.source_pool, index=h.source_slots)
+        plan.launch_batch(src, pool_rows(want, block_table=bt, page_size=16), spans)
+        tgt = pool_rows(got, block_table=bt, page_size=16)
+        arr = _span_array(spans)
+        _lib.check(lib.cb_map_install_batch_noalloc(plan._handle, ctypes.byref(src.c),
+                                                    ctypes.byref(tgt.c), arr, len(spans),
+                                                    _lib.stream_handle(stream)))
+        torch.cuda.synchronize()
+        assert plan.read_errors() == 0
+        assert torch.equal(got.k_data, want.k_data)
+        assert torch.equal(got.v_data, want.v_data)
+        assert int(got.v_data.abs().sum()) > 0
+        del want, got
 
 
 def test_noalloc_batch_beyond_the_workspace_is_rejected_before_launch():
