@@ -73,3 +73,29 @@ def test_pool_installs_every_row_over_many_launches():
     assert h.mapper.plan.read_errors() == 0
     assert torch.equal(fs.snapshot(pool, slots), ref)
     fs.check_untouched(pool, written)
+
+
+def test_pool_on_a_capped_grid_matches_the_full_grid():
+    """A cap on tokens per workgroup shrinks the grid: the TP4 share at 4096
+    tokens with 16,384 unit-tokens per workgroup runs on 32 workgroups, each
+    with about 26K weight units of work (a pool), where the default grid of
+    256 has about 3.2K (no pool). Both write the same rows bit for bit."""
+    sh = synthetic.shape("tp4")
+    n = sh.tokens
+    print(f"capped grid: {sh.target_layers}x{sh.target_heads}, {n} tokens, 16384 unit-tokens per workgroup",
+          flush=True)
+    h = synthetic.make_handoff(sh, target_pages=1024, device_source=True)
+    pool = h.target_pool
+    slots = synthetic.slots_from_pages(h.block_table.cpu(), n, sh.page_size).to(pool.k_data.device)
+    written = [slots] * sh.target_layers
+
+    fs.fill_sentinel(pool)
+    h.run()
+    assert h.mapper.plan.read_errors() == 0
+    ref = fs.snapshot(pool, slots)
+    for i in range(3):
+        fs.fill_sentinel(pool)
+        h.run(tokens_per_workgroup=16384)
+        assert h.mapper.plan.read_errors() == 0
+        assert torch.equal(fs.snapshot(pool, slots), ref), f"capped launch {i}"
+    fs.check_untouched(pool, written)
