@@ -152,6 +152,40 @@ def host_cpu() -> dict:
             "affinity_cpus": len(os.sched_getaffinity(0)), "sockets": len(sockets) or None}
 
 
+def _cpu_batch(workload: str, count: int | None = None):
+    """CPU-oracle handoffs of the seeded ragged requests (``count`` first, all 64
+    by default), one request after another, as a callable returning the summed
+    seconds and the tokens mapped."""
+    import torch
+
+    from cachebridge_amd import synthetic
+    from oracle import install as oi
+
+    lengths = synthetic.request_lengths()
+    lengths = lengths if count is None else lengths[:count]
+    sh = synthetic.shape(workload, tokens=max(lengths))
+    spec = synthetic.mapper_spec(sh)
+    longest = max(lengths)
+    values = synthetic.source_values(sh)
+    src = oi.RowStorePool(sh.source_layers, longest, sh.source_heads, sh.head_dim, dtype=sh.dtype,
+                          fill=values)
+    del values
+    tgt = oi.RowStorePool(sh.target_layers, longest, sh.target_heads, sh.head_dim, dtype=sh.dtype)
+    slots = torch.randperm(longest, generator=torch.Generator().manual_seed(5))
+
+    def once() -> float:
+        total = 0.0
+        for n in lengths:
+            t0 = time.perf_counter()
+            oi.map_install_oracle(src, torch.arange(n), tgt, slots[:n], spec, position_start=0,
+                                  source_theta=sh.source_theta, target_thetas=sh.target_theta,
+                                  windows=sh.windows, prefix_length=n)
+            total += time.perf_counter() - t0
+        return total
+
+    return once, sum(lengths)
+
+
 def _cpu_handoff(workload: str, tokens: int):
     """One full CPU-oracle handoff of ``workload`` as a callable returning seconds."""
     import torch
@@ -221,6 +255,14 @@ def cpu_baseline(workload: str, tokens: int, *, runs: int = 5, extra: bool = Tru
            "single_thread_value": round(tokens / single, 1)}
     if extra:
         configs = {}
+        # C4: the 64 seeded ragged requests (137,440 tokens, TP4 share), one
+        # CPU handoff per request, summed; one run (about 10 s at 16 threads).
+        batch_once, batch_tokens = _cpu_batch("batch")
+        batch_s, _ = _timed_cpu(batch_once, all_cpus, 1, warm=False)
+        configs["batch"] = {"tokens": batch_tokens, "label": "batch: 64 requests summed, TP4 share",
+                            "handoff_s": round(batch_s, 4), "tokens_per_s": round(batch_tokens / batch_s, 1),
+                            "runs": 1, "threads": all_cpus}
+        del batch_once
         for name, t in (("toy", 256), ("gemma", 8192), ("full32k", 32768)):
             label = name
             probe = _cpu_handoff(name, t)
@@ -235,7 +277,77 @@ def cpu_baseline(workload: str, tokens: int, *, runs: int = 5, extra: bool = Tru
             del probe
             configs[name] = {"tokens": t, "label": label, "handoff_s": round(med, 4),
                              "tokens_per_s": round(t / med, 1), "runs": n, "threads": all_cpus}
+        # One thread (the reference CI's OMP_NUM_THREADS=1) on a bounded
+        # sample of every configuration, a few seconds each.
+        single = {}
+        for name, t in (("toy", 256), ("full", 1024), ("gemma", 512)):
+            probe = _cpu_handoff(name, t)
+            sec, _ = _timed_cpu(probe, 1, 1, warm=False)
+            del probe
+            single[name] = {"tokens": t, "handoff_s": round(sec, 4), "tokens_per_s": round(t / sec, 1)}
+        batch_once, batch_tokens = _cpu_batch("batch", count=4)
+        sec, _ = _timed_cpu(batch_once, 1, 1, warm=False)
+        single["batch"] = {"tokens": batch_tokens, "requests": 4, "handoff_s": round(sec, 4),
+                           "tokens_per_s": round(batch_tokens / sec, 1)}
+        del batch_once
         out["configs"] = configs
+        single["tp4"] = {"tokens": tokens, "handoff_s": round(tokens / out["single_thread_value"], 4),
+                         "tokens_per_s": out["single_thread_value"]} if workload == "tp4" else None
+        out["single_thread"] = {"threads": 1, "sample": "the first `tokens` tokens of each configuration "
+                                "(toy and the TP4 share in full; full stands for full32k too, the same "
+                                "40x8 -> 64x8 geometry; batch: its first 4 requests summed)",
+                                "configs": single}
+    return out
+
+
+SAMPLE_LAYERS = [0, 1, 17, 31, 32, 47, 62, 63]
+
+
+def sampled_parity(h, sh, label: str) -> dict:
+    """Oracle check of the installed rows of the benchmarked handoff.
+
+    Part of the CPU-baseline leg (the oracle is the checker here, never the
+    thing measured): after the timed region, the CPU oracle maps the first,
+    middle and last 64 tokens of the history (and both sides of any window
+    edge) for 8 target layers, all heads, K and V, from the source rows read
+    back from the GPU pool, and the GPU's installed rows at those tokens' slots
+    are compared with it to the parity bar of ``oracle.tolerance.check_mapped``
+    (1 bf16 ulp, or 2^-14 of the summand magnitude for near-cancelling
+    elements; >= 99.9% within 1 ulp; normwise and element-wise relative error
+    <= 1e-2).
+    """
+    import torch
+
+    from cachebridge_amd import synthetic
+    from tests import fullsize as fs
+
+    n = sh.tokens
+    dev = h.target_pool.k_data.device
+    tgt_slots = synthetic.slots_from_pages(h.block_table.cpu(), n, sh.page_size).to(dev)
+    first = fs.first_kept(sh.windows, sh.target_layers, prefix=n)
+    layers = [l for l in SAMPLE_LAYERS if l < sh.target_layers]
+    h.run()
+    torch.cuda.synchronize()
+    if h.mapper.plan.read_errors() != 0:
+        raise RuntimeError("kernel flagged out-of-range rows")
+    out = {"workload": label, "sample": f"tokens {fs.token_windows(n, edges=sorted({f for f in first if f}))} "
+                                        f"x target layers {layers} x all heads x K/V"}
+    try:
+        stats = []
+        for lo, hi in fs.token_windows(n, edges=sorted({f for f in first if f})):
+            stats += fs.oracle_window(h.source_pool, h.source_slots, h.target_pool, tgt_slots, h.spec,
+                                      lo=lo, hi=hi, position_start=0, layers=layers,
+                                      source_theta=sh.source_theta, target_thetas=sh.target_theta,
+                                      first=first)
+        summary = fs.summarize(stats)
+        out.update(ok=True, elements=summary["elements"], within_1ulp=round(summary["within_1ulp"], 6),
+                   beyond_1ulp_fraction=round(summary["beyond_1ulp_fraction"], 6),
+                   max_ulp=summary["max_ulp"], max_rel_norm=round(summary["max_rel_norm"], 6),
+                   max_rel_elem=round(summary["max_rel_elem"], 6),
+                   rel_elem_fraction=round(summary["rel_elem_fraction"], 6),
+                   rel_elem_rule="elements with |ref| >= 100 x their near-cancellation allowance")
+    except AssertionError as e:
+        out.update(ok=False, error=str(e)[:400])
     return out
 
 
@@ -805,23 +917,37 @@ def main() -> int:
     }
     if not args.workload.startswith("batch"):
         line["publish_ready_ms"] = publish_ready_latency(h)
+        if not args.no_cpu_baseline:
+            line["parity"] = sampled_parity(h, sh, args.workload)
     del h
     torch.cuda.empty_cache()
     if not args.no_north_star and args.workload == "tp4":
         ns = synthetic.shape("full", tokens=4096)
         hn = synthetic.make_handoff(ns)
-        wall_n, kms_n, lat_n, _ = time_handoff(hn, max(20, args.steps // 4), args.warmup)
+        steps_n = max(20, args.steps // 4)
+        wall_n, kms_n, lat_n, lat_min_n = time_handoff(hn, steps_n, args.warmup)
         b = synthetic.algorithmic_bytes(ns)
+        traffic_n, traffic_src_n = profiled_traffic("map_install_stream", "full")
+        gbs_n = b / (kms_n * 1e-3) / 1e9
         line["north_star_64x8"] = {
-            "workload": WORKLOADS["full"], "kernel_ms_mean": round(kms_n, 4),
-            "handoff_latency_ms": round(lat_n, 4),
+            "workload": WORKLOADS["full"], "steps": steps_n, "kernel_ms_mean": round(kms_n, 4),
+            "handoff_latency_ms": round(lat_n, 4), "handoff_latency_min_ms": round(lat_min_n, 4),
             "tokens_per_s": round(ns.tokens / (kms_n * 1e-3), 1),
-            "hbm_frac": round(b / (kms_n * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "wall_tokens_per_s": round(steps_n * ns.tokens / wall_n, 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs_n, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs_n / HBM_PEAK_GBS, 4), "traffic": traffic_n,
+                         "traffic_source": traffic_src_n, "kernel": "map_install_stream_kernel<128, bf16>",
+                         "algorithmic_bytes_per_launch": b, "kernel_ms_mean": round(kms_n, 5)},
+            "hbm_frac": round(gbs_n / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_launch": b,
-            "traffic": profiled_traffic("map_install_stream", "full")[0],
+            "traffic": traffic_n,
         }
+        if not args.no_cpu_baseline:
+            line["north_star_64x8"]["parity"] = sampled_parity(hn, ns, "full")
         del hn
         torch.cuda.empty_cache()
+        if not args.no_cpu_baseline:
+            line["north_star_64x8"]["cpu_baseline"] = cpu_baseline("full", 4096, runs=3, extra=False)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload, tokens)
         line["gpu_over_cpu"] = round(value / line["cpu_baseline"]["value"], 1)

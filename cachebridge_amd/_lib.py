@@ -132,6 +132,7 @@ SIGNATURES = {
     "cb_plan_create": (ctypes.c_int, [ctypes.POINTER(CbPlanDesc), ctypes.POINTER(_c_void_p)]),
     "cb_plan_destroy": (None, [_c_void_p]),
     "cb_plan_get_info": (ctypes.c_int, [_c_void_p, ctypes.POINTER(CbPlanInfo)]),
+    "cb_plan_last_split": (ctypes.c_int, [_c_void_p, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "cb_map_install": (ctypes.c_int, [_c_void_p, ctypes.POINTER(CbRequest), _c_void_p]),
     "cb_batch_workspace_bytes": (ctypes.c_int, [_c_void_p, ctypes.POINTER(CbSpan), _i32,
                                                 ctypes.POINTER(_i64)]),

@@ -1003,12 +1003,19 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
   }
   // The last workgroup to finish clears the launch's counter pair (every
   // claim of the launch has been made by then), so the next launch on this
-  // pair starts from zero without a host-side clear.
+  // pair starts from zero without a host-side clear. A launch that had the
+  // pair to itself made exactly pool_n successful claims plus one failed
+  // claim per workgroup; any other count means another launch shared the
+  // pair (chunks may have gone to it and rows may be missing), which is
+  // reported in bit 3 of the error word instead of passing silently.
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(a.pool_ctr + 1, 1u);
     if (done == gridDim.x - 1) {
-      atomicExch(a.pool_ctr, 0u);
+      const uint32_t claims = atomicExch(a.pool_ctr, 0u);
       atomicExch(a.pool_ctr + 1, 0u);
+      if (claims != static_cast<uint32_t>(a.pool_n) + gridDim.x) atomicOr(a.err, 8);
+    } else if (done >= gridDim.x) {
+      atomicOr(a.err, 8);
     }
   }
 }
@@ -2287,7 +2294,8 @@ static_assert(3 * ((int64_t{CB_NOALLOC_MAX_TOKENS} * 4 + 255) / 256 * 256) <= CB
 // Host side
 // ---------------------------------------------------------------------------
 
-constexpr int kPoolSlots = 64;  // work-pool counter pairs per plan
+constexpr int kPoolSlots = 64;     // work-pool counter pairs that direct launches rotate over
+constexpr int kCapturePairs = 64;  // further pairs, each given to one launch recorded into a HIP graph
 
 struct cb_plan {
   int device = 0;
@@ -2319,10 +2327,18 @@ struct cb_plan {
   mutable std::mutex split_mu;
   mutable std::vector<int32_t> split_key, split_unit, split_sub;
   mutable int32_t split_pool[4] = {0, 0, 0, 0};  // pool_n, pool_u0, pool_s0, pool_gs
-  // Work-pool counters of the streaming kernel: kPoolSlots pairs (claims,
-  // finished workgroups), zero between launches; launch k uses pair k % kPoolSlots.
+  // Work-pool counters of the streaming kernel: kPoolSlots + kCapturePairs
+  // pairs (claims, finished workgroups), zero between launches. Direct
+  // launch k uses pair k % kPoolSlots. A launch recorded into a HIP graph
+  // keeps its pair for every replay, so each one gets a pair of its own from
+  // the capture range, which direct launches never use; once that range is
+  // spent, captured launches run without the pool (static ranges only).
   uint32_t* d_pool = nullptr;
   mutable std::atomic<uint32_t> pool_seq{0};
+  mutable std::atomic<uint32_t> capture_seq{0};
+  // The last launch's split, for callers and tests (cb_plan_last_split).
+  mutable std::atomic<int32_t> last_pool_chunks{0};
+  mutable std::atomic<int32_t> last_workgroups{0};
   float* d_cos = nullptr;
   float* d_sin = nullptr;
   float* d_ucos = nullptr;
@@ -2528,8 +2544,9 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     if (group_unit_count[unit_group[u]] == 1) w = (w * 13 + 5) / 10;
     p->unit_weight[u] = w;
   }
-  if ((rc = upload(&p->d_pool, nullptr, 2 * kPoolSlots * sizeof(uint32_t), &bytes))) return rc;
-  CB_HIP(hipMemset(p->d_pool, 0, 2 * kPoolSlots * sizeof(uint32_t)));
+  const size_t pool_bytes = 2 * (kPoolSlots + kCapturePairs) * sizeof(uint32_t);
+  if ((rc = upload(&p->d_pool, nullptr, pool_bytes, &bytes))) return rc;
+  CB_HIP(hipMemset(p->d_pool, 0, pool_bytes));
   int32_t* d_order = nullptr;
   CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), order.size() * 4));
   hipError_t e = hipMemcpy(d_order, order.data(), order.size() * 4, hipMemcpyHostToDevice);
@@ -2663,7 +2680,7 @@ constexpr int64_t kSegmentCost = 256;
 // budget), so ranges that cross a unit boundary get fewer sub-tiles. With a
 // work pool, the ranges are filled to a smaller budget and the rest of the
 // line becomes the pool (a->pool_*).
-void split_cost_line(const cb_plan* p, MapArgs* a) {
+void split_cost_line(const cb_plan* p, MapArgs* a, bool allow_pool) {
   const int nu = p->num_units, nb = a->num_blocks;
   std::vector<int32_t> ns(nu, 0);
   int64_t total = 0;
@@ -2723,7 +2740,8 @@ void split_cost_line(const cb_plan* p, MapArgs* a) {
     else lo = mid + 1;
   }
   int64_t pool_pct = 0, chunk_pct = 0;
-  if (lo >= CB_POOL_LONG_BUDGET) {
+  if (!allow_pool) {
+  } else if (lo >= CB_POOL_LONG_BUDGET) {
     pool_pct = CB_POOL_LONG_PCT;
     chunk_pct = CB_POOL_LONG_CHUNK_PCT;
   } else if (lo >= CB_POOL_MID_BUDGET) {
@@ -2836,7 +2854,21 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
       nb = std::min<int64_t>(nb, std::max<int64_t>(8, (unit_tokens + chunk - 1) / chunk));
     a.num_blocks = static_cast<int32_t>(std::max<int64_t>(8, nb / 8 * 8));
     grid_blocks = a.num_blocks;
-    std::vector<int32_t> key{a.num_blocks, p->num_windows};
+    // A launch recorded into a HIP graph keeps its counter pair for every
+    // replay: it takes a pair of its own from the capture range, or runs
+    // without the pool once that range is spent.
+    bool allow_pool = true, captured = false;
+    uint32_t capture_pair = 0;
+    {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      CB_HIP(hipStreamIsCapturing(s, &cs));
+      if (cs != hipStreamCaptureStatusNone) {
+        captured = true;
+        capture_pair = p->capture_seq.fetch_add(1, std::memory_order_relaxed);
+        allow_pool = capture_pair < static_cast<uint32_t>(kCapturePairs);
+      }
+    }
+    std::vector<int32_t> key{a.num_blocks, p->num_windows, allow_pool ? 1 : 0};
     for (int c = 0; c < p->num_windows; ++c) key.push_back(a.cls_subtiles[c]);
     const size_t nbk = static_cast<size_t>(a.num_blocks) + 1;
     std::lock_guard<std::mutex> lock(p->split_mu);
@@ -2848,7 +2880,7 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
       a.pool_s0 = p->split_pool[2];
       a.pool_gs = p->split_pool[3];
     } else {
-      split_cost_line(p, &a);
+      split_cost_line(p, &a, allow_pool);
       p->split_key = key;
       p->split_unit.assign(a.blk_unit, a.blk_unit + nbk);
       p->split_sub.assign(a.blk_sub, a.blk_sub + nbk);
@@ -2857,8 +2889,13 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
       p->split_pool[2] = a.pool_s0;
       p->split_pool[3] = a.pool_gs;
     }
-    a.pool_ctr = p->d_pool + 2 * (p->pool_seq.fetch_add(1, std::memory_order_relaxed) % kPoolSlots);
+    // (Without the pool the kernel never touches its pair.)
+    const uint32_t pair = captured ? (allow_pool ? static_cast<uint32_t>(kPoolSlots) + capture_pair : 0u)
+                                   : p->pool_seq.fetch_add(1, std::memory_order_relaxed) % kPoolSlots;
+    a.pool_ctr = p->d_pool + 2 * static_cast<size_t>(pair);
   }
+  p->last_pool_chunks.store(ws ? a.pool_n : 0, std::memory_order_relaxed);
+  p->last_workgroups.store(static_cast<int32_t>(grid_blocks), std::memory_order_relaxed);
   const dim3 grid(static_cast<unsigned>(grid_blocks)), block(ws ? kStreamThreads : kThreads);
   if (ws) {
     const bool pv = a.pos != nullptr;
@@ -3082,6 +3119,13 @@ void cb_plan_destroy(cb_plan* plan) { plan_free(plan); }
 int cb_plan_get_info(const cb_plan* plan, cb_plan_info* info) {
   if (!plan || !info) return fail(CB_EINVAL, "null plan or info");
   *info = plan->info;
+  return CB_OK;
+}
+
+int cb_plan_last_split(const cb_plan* plan, int32_t* pool_chunks, int32_t* workgroups) {
+  if (!plan || !pool_chunks || !workgroups) return fail(CB_EINVAL, "null plan or output");
+  *pool_chunks = plan->last_pool_chunks.load(std::memory_order_relaxed);
+  *workgroups = plan->last_workgroups.load(std::memory_order_relaxed);
   return CB_OK;
 }
 

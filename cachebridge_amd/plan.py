@@ -414,8 +414,23 @@ class HandoffPlan:
         source.hold_for(s)
         target.hold_for(s)
 
+    def last_split(self) -> tuple[int, int]:
+        """``(pool_chunks, workgroups)`` of this plan's last map launch.
+
+        ``pool_chunks`` is the number of work-pool chunks that launch's
+        workgroups claimed dynamically (0: static ranges only).
+        """
+        chunks, groups = ctypes.c_int32(0), ctypes.c_int32(0)
+        _lib.check(self.lib.cb_plan_last_split(self._handle, ctypes.byref(chunks), ctypes.byref(groups)))
+        return int(chunks.value), int(groups.value)
+
     def read_errors(self, stream: torch.cuda.Stream | None = None) -> int:
-        """Synchronize ``stream`` and return/clear the device out-of-range flags."""
+        """Synchronize ``stream`` and return/clear the device error flags.
+
+        Bit 0: a source row out of range; bit 1: a target row out of range;
+        bit 2: a kernel's internal schedule failed; bit 3: a streaming launch
+        shared its work-pool counter pair with another launch in flight.
+        """
         flags = ctypes.c_int32(0)
         _lib.check(self.lib.cb_plan_read_errors(self._handle, ctypes.byref(flags),
                                                 _lib.stream_handle(stream)))

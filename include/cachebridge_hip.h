@@ -152,7 +152,14 @@ typedef struct cb_request {
   int32_t num_tokens;
   int32_t position_start;
   int32_t prefix_length; /* whole prefix length for windows; 0 means position_start + num_tokens */
-  int32_t tokens_per_workgroup; /* 0 = library default; else a multiple of 128 */
+  /* 0 = library default. Otherwise a cap on the tokens each workgroup maps
+     per unit of work: a positive multiple of 16 for the streaming kernel
+     (bf16 / fp32 maps with support 1 at head_dim 64 or 128) and of 32 for the
+     generic kernels; the support kernel (support > 1 at head_dim 128, bf16)
+     ignores it. For the streaming kernel a cap below the default shrinks the
+     grid to about (tokens x units) / cap workgroups, which can make each
+     workgroup's share long enough for the work pool. */
+  int32_t tokens_per_workgroup;
 } cb_request;
 
 typedef struct cb_plan cb_plan;
@@ -173,6 +180,11 @@ int cb_abi_version(void);
 int cb_plan_create(const cb_plan_desc* desc, cb_plan** out);
 void cb_plan_destroy(cb_plan* plan);
 int cb_plan_get_info(const cb_plan* plan, cb_plan_info* info);
+/* Work split of the plan's last map launch (host-side values, no device
+   access): the work-pool chunks its workgroups claimed dynamically (0: static
+   ranges only) and its workgroups. No counterpart in the reference; it lets
+   a caller or test see which scheduling a launch used. */
+int cb_plan_last_split(const cb_plan* plan, int32_t* pool_chunks, int32_t* workgroups);
 
 /* Fused gather -> un-rotate -> MFMA affine map -> bias -> rotate -> cast ->
    scatter for every job of the plan over one request block. Asynchronous. */
@@ -262,7 +274,18 @@ int cb_delta_state_transform(int32_t dtype, int64_t batch, int32_t k, int32_t v,
 /* Read and clear the plan's device error word (bit 0: source row out of
    range, bit 1: target row out of range, bit 2: a kernel's internal schedule
    failed -- a bounded wait of the support kernel timed out, or a work-pool
-   claim of the streaming kernel fell past its pool). Synchronizes `stream`. */
+   claim of the streaming kernel fell past its pool; bit 3: a streaming
+   launch found its work-pool counter pair shared with another launch of the
+   plan in flight, so rows may be missing). The word is one per plan: bits
+   from launches that overlap are merged. Synchronizes `stream`.
+
+   Work-pool counters: direct launches of one plan rotate over 64 counter
+   pairs, so up to 64 of them may be in flight at once on any streams; a
+   launch recorded into a HIP graph takes a pair of its own (64 per plan;
+   later captured launches run without the pool), so graph replays never
+   share a pair with direct launches. Two replays of one graph that overlap
+   in time do share their pair, and more than 64 direct launches in flight
+   share pairs: such launches set bit 3. */
 int cb_plan_read_errors(cb_plan* plan, int32_t* flags, void* stream);
 
 #ifdef __cplusplus

@@ -12,6 +12,12 @@ therefore accepts an element when its bf16 (or fp16, for fp16 pools) bit
 patterns are at most one ulp apart **or** ``|out - ref| <= abs_factor * bound``, where ``bound`` is the
 magnitude of the chain's summands (``magnitude_bound``), and separately
 requires a normwise relative error ``max|out-ref| / max|ref| <= 1e-2``.
+It also reports, and bounds by the same 1e-2, the element-wise relative
+error ``|out-ref| / |ref|`` over the elements whose magnitude is at least
+``1 / rel_norm`` times their near-cancellation allowance (``abs_factor *
+bound``): there the allowance itself is at most 1e-2 of the value, so a
+larger relative error would be a real defect rather than a legitimately
+reordered sum.
 """
 
 from __future__ import annotations
@@ -93,6 +99,11 @@ def check_mapped(out: torch.Tensor, ref: torch.Tensor, bound: torch.Tensor, *,
     allowed = diff <= abs_factor * bound
     stats = {"elements": o.numel(), "max_abs": float(diff.max()),
              "rel_norm": float(diff.max() / r.double().abs().max().clamp_min(1e-30))}
+    mag = r.double().abs()
+    sized = (mag > 0) & (mag >= (abs_factor / rel_norm) * bound)
+    rel = diff[sized] / mag[sized]
+    stats["max_rel_elem"] = float(rel.max()) if rel.numel() else 0.0
+    stats["rel_elem_fraction"] = float(sized.double().mean())
     if o.dtype in (torch.bfloat16, torch.float16):
         ulp = ulp_distance(o, r)
         within = ulp <= 1
@@ -106,5 +117,6 @@ def check_mapped(out: torch.Tensor, ref: torch.Tensor, bound: torch.Tensor, *,
     stats["violations"] = bad
     assert bad == 0, f"{bad} elements outside tolerance: {stats}"
     assert stats["rel_norm"] <= rel_norm, stats
+    assert stats["max_rel_elem"] <= rel_norm, stats
     assert stats["within_1ulp"] >= min_within_ulp, stats
     return stats

@@ -128,4 +128,7 @@ def summarize(stats: list[dict]) -> dict:
     return {"checks": len(stats), "elements": elems, "within_1ulp": within,
             "beyond_1ulp_fraction": 1.0 - within,
             "max_ulp": max((s["max_ulp"] for s in stats), default=0),
-            "max_rel_norm": max((s["rel_norm"] for s in stats), default=0.0)}
+            "max_rel_norm": max((s["rel_norm"] for s in stats), default=0.0),
+            "max_rel_elem": max((s["max_rel_elem"] for s in stats), default=0.0),
+            "rel_elem_fraction": (sum(s["rel_elem_fraction"] * s["elements"] for s in stats)
+                                  / max(elems, 1))}

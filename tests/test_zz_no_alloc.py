@@ -111,6 +111,58 @@ def test_noalloc_pooled_batch_equals_allocating_batch():
         del want, got
 
 
+def test_noalloc_pooled_batch_replays_from_a_hip_graph():
+    """The no-allocation call recorded into a HIP graph (torch.cuda.graph) on
+    a batch long enough for the work pool, replayed four times with eager
+    launches of the same plan on another stream and host synchronizations in
+    between: every replay writes exactly the rows of a direct launch, and the
+    error word stays clear. A captured launch takes a counter pair of its own,
+    which the direct launches never rotate onto."""
+    lib = _lib.load()
+    lengths, positions = [1500, 2000, 900, 700], [0, 0, 64, 3]
+    tokens = sum(lengths)
+    sh = synthetic.shape("full", tokens=tokens)
+    pages = sum((n + 15) // 16 for n in lengths) * 2
+    h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros", device_source=True)
+    plan = h.mapper.plan
+    spans, bt = _spans(lengths, positions, pages, seed=60)
+    bt = bt.to(h.target_pool.device)
+    src = pool_rows(h.source_pool, index=h.source_slots)
+    want = _zero_pool_like(h.target_pool)
+    print(f"graph replay: {len(lengths)} requests, {tokens} tokens, whole model", flush=True)
+    plan.launch_batch(src, pool_rows(want, block_table=bt, page_size=16), spans)
+    torch.cuda.synchronize()
+    assert plan.last_split()[0] > 0, "the batch must be long enough for the work pool"
+    assert plan.read_errors() == 0
+
+    got = _zero_pool_like(h.target_pool)
+    tgt = pool_rows(got, block_table=bt, page_size=16)
+    arr = _span_array(spans)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    other = _zero_pool_like(h.target_pool)
+    other_rows = pool_rows(other, block_table=bt, page_size=16)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        _lib.check(lib.cb_map_install_batch_noalloc(plan._handle, ctypes.byref(src.c),
+                                                    ctypes.byref(tgt.c), arr, len(spans),
+                                                    _lib.stream_handle(torch.cuda.current_stream())))
+    for replay in range(4):
+        got.k_data.zero_()
+        got.v_data.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        with torch.cuda.stream(side):
+            plan.launch_batch(src, other_rows, spans)
+        torch.cuda.synchronize()
+        print(f"replay {replay}", flush=True)
+        assert plan.read_errors() == 0
+        assert torch.equal(got.k_data, want.k_data)
+        assert torch.equal(got.v_data, want.v_data)
+        assert torch.equal(other.k_data, want.k_data)
+    del graph
+
+
 def test_noalloc_batch_beyond_the_workspace_is_rejected_before_launch():
     lib = _lib.load()
     sh = synthetic.shape("tp4", tokens=64)
