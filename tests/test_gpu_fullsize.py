@@ -87,14 +87,18 @@ def test_full_size_handoff(name, layers):
     fs.check_untouched(pool, written)
 
 
-def test_full_size_ragged_batch():
-    sh = synthetic.shape("batch")
-    b = synthetic.make_batch_handoff(sh)  # 64 requests, pool at 85% occupancy
+@pytest.mark.parametrize("name", ["batch", "batch_full"])
+def test_full_size_ragged_batch(name):
+    """64 ragged requests in one launch: at the TP4 share into one pool at 85%
+    occupancy, and at the whole-model 40x8 -> 64x8 geometry into a pool at
+    50% occupancy (85% would need 260 GB next to the source pool)."""
+    sh = synthetic.shape(name)
+    b = synthetic.make_batch_handoff(sh)
     pool = b.target_pool
     dev = pool.k_data.device
     ps = sh.page_size
-    print(f"full-size batch: {len(b.lengths)} requests, {b.tokens} tokens, {pool.pages} pages",
-          flush=True)
+    print(f"full-size {name}: {len(b.lengths)} requests, {b.tokens} tokens, {sh.target_layers}x"
+          f"{sh.target_heads}, {pool.pages} pages", flush=True)
     assert len(b.lengths) == 64
     src_of, tgt_of = [], []
     for sp in b.spans:
@@ -124,7 +128,7 @@ def test_full_size_ragged_batch():
                                       hi=hi, position_start=sp.position_start, layers=SAMPLE_64,
                                       source_theta=sh.source_theta, target_thetas=sh.target_theta,
                                       first=no_window)
-    print("batch oracle", sorted(picks), fs.summarize(stats), flush=True)
+    print(name, "oracle", sorted(picks), fs.summarize(stats), flush=True)
 
     batched = fs.snapshot(pool, all_tgt)
     fs.fill_sentinel(pool)

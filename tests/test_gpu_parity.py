@@ -55,6 +55,52 @@ def test_map_page_matches_reference_golden(golden_dir, name):
     print(name, stats)
 
 
+def test_toy_golden_installed_through_a_random_block_table(golden_dir):
+    """The toy configuration (8x2 -> 12x2, D 64, 256 fp32 tokens) through the
+    paged install: the reference's golden source page is mapped straight into
+    a page-16 target pool through a seeded random-permutation block table over
+    three times the pages the request needs. The rows at the block table's
+    slots must equal the reference's golden ``map_page`` output to the fp32
+    parity bar, and every other row of the pool must keep its bits."""
+    from cachebridge_amd.plan import rows_from_page
+    from cachebridge_amd.pool import PagedKVPool, pool_rows
+
+    man, g = _golden(golden_dir, "toy_fp32")
+    spec = {k: g[k] for k in SPEC_KEYS}
+    page = g["page"]
+    lt, ht = spec["assign_layer"].shape[:2]
+    n, dim = page.shape[2], page.shape[4]
+    need = (n + 15) // 16
+    pages = 3 * need
+    mapper = HeadwiseMapper.from_assignment(
+        **spec, source_rope_theta=man["source_theta"], target_rope_theta=man["target_theta"],
+        dtype=torch.float32, device="cuda", max_positions=4096)
+    pool = PagedKVPool(layer_num=lt, pages=pages, head_num=ht, head_dim=dim, page_size=16,
+                       dtype=torch.float32, device="cuda", fill=None)
+    gen = torch.Generator().manual_seed(77)
+    pool.k_data.copy_(torch.randn(pool.k_data.shape, generator=gen))
+    pool.v_data.copy_(torch.randn(pool.v_data.shape, generator=gen))
+    before_k, before_v = pool.k_data.clone(), pool.v_data.clone()
+    bt = torch.randperm(pages, generator=gen)[:need].to(torch.int32)
+    slots = synthetic.slots_from_pages(bt, n, 16).cuda()
+    source = rows_from_page(page.cuda())
+    target = pool_rows(pool, block_table=bt.cuda(), page_size=16, tokens=n)
+    mapper.map_install(source, target, num_tokens=n, position_start=man["position_start"])
+    torch.cuda.synchronize()
+    assert mapper.plan.read_errors() == 0
+    got = torch.stack([torch.stack([b[slots] for b in pool.k_buffer]),
+                       torch.stack([b[slots] for b in pool.v_buffer])]).cpu()
+    bound = ot.magnitude_bound(page, spec, position_start=man["position_start"],
+                               source_theta=man["source_theta"], target_thetas=man["target_theta"])
+    stats = ot.check_mapped(got, g["out"], bound, abs_factor=_factor(torch.float32))
+    print("toy via block table", stats)
+    rest = torch.ones(pool.k_buffer[0].shape[0], dtype=torch.bool, device="cuda")
+    rest[slots] = False
+    for l in range(lt):
+        assert torch.equal(pool.k_buffer[l][rest], before_k[l][rest])
+        assert torch.equal(pool.v_buffer[l][rest], before_v[l][rest])
+
+
 def test_reference_artifact_s8_tp_slice_matches_golden(golden_dir):
     man, g = _golden(golden_dir, "slice_bf16_s8")
     files = [{"selected": g["selected"], "k_weight": g["k_weight"], "k_bias": g["k_bias"],

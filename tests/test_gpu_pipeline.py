@@ -2,7 +2,11 @@
 
 Both paths run the same map kernel arithmetic per (target layer, head, kind),
 so the target pools must be bit-identical, including rows outside each
-sliding window (left untouched by both) and rows outside the request.
+sliding window (left untouched by both) and rows outside the request. The
+staged pipeline's own rows are also compared with the oracle on sampled token
+windows (first, middle and last 64 tokens and both sides of each window
+edge), every target layer, all heads, K and V, to the parity bar of
+``oracle.tolerance.check_mapped``.
 """
 
 from __future__ import annotations
@@ -13,6 +17,7 @@ import torch
 from cachebridge_amd import synthetic
 from cachebridge_amd.online.pipeline import StagedHandoff
 from cachebridge_amd.pool import pool_rows
+from tests import fullsize as fs
 
 pytestmark = pytest.mark.gpu
 
@@ -37,8 +42,10 @@ def test_staged_pipeline_equals_fused_install(name, tokens, layers, chunk, block
     sh = _shape(name, tokens, layers)
     pages = (tokens + 15) // 16 * 3
     fused = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros")
+    fs.fill_sentinel(fused.target_pool)
     fused.run()
     staged_h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros")
+    fs.fill_sentinel(staged_h.target_pool)
     width = max(b - a for a, b in blocks)
     staged = StagedHandoff(staged_h.mapper, layer_chunk=chunk, max_tokens=width)
     assert staged.staging_bytes == 2 * 2 * chunk * width * sh.target_heads * sh.head_dim * 2
@@ -53,8 +60,19 @@ def test_staged_pipeline_equals_fused_install(name, tokens, layers, chunk, block
     for plan in staged.plans:
         assert plan.read_errors() == 0
     assert fused.mapper.plan.read_errors() == 0
-    assert torch.equal(staged_h.target_pool.k_data, fused.target_pool.k_data)
-    assert torch.equal(staged_h.target_pool.v_data, fused.target_pool.v_data)
+    assert torch.equal(staged_h.target_pool.k_data.view(torch.int16), fused.target_pool.k_data.view(torch.int16))
+    assert torch.equal(staged_h.target_pool.v_data.view(torch.int16), fused.target_pool.v_data.view(torch.int16))
+
+    dev = staged_h.target_pool.k_data.device
+    tgt_slots = synthetic.slots_from_pages(staged_h.block_table.cpu(), tokens, 16).to(dev)
+    first = fs.first_kept(sh.windows, sh.target_layers, prefix=tokens)
+    stats = []
+    for lo, hi in fs.token_windows(tokens, edges=sorted({f for f in first if f})):
+        stats += fs.oracle_window(staged_h.source_pool, staged_h.source_slots, staged_h.target_pool,
+                                  tgt_slots, staged_h.spec, lo=lo, hi=hi, position_start=0,
+                                  layers=list(range(sh.target_layers)), source_theta=sh.source_theta,
+                                  target_thetas=sh.target_theta, first=first)
+    print("staged oracle", fs.summarize(stats), flush=True)
 
 
 def test_staged_pipeline_rejects_oversized_block():

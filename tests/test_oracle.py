@@ -244,3 +244,38 @@ def test_tolerance_accepts_one_fp16_ulp_and_rejects_two():
     ot.check_mapped((bits + 1).view(torch.float16), ref, tiny, min_within_ulp=1.0)
     with pytest.raises(AssertionError):
         ot.check_mapped((bits + 2).view(torch.float16), ref, tiny)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_row_store_writes_exactly_its_inputs_at_loc(dtype):
+    """The oracle's SGLang row-store stand-in (``set_kv_buffer``): the rows at
+    ``loc`` of the named layer become exactly the given K and V rows (cast to
+    the pool dtype when they arrive in another), every other row of that layer
+    and every row of every other layer keep their bits, for int64 and int32
+    ``loc`` in any order."""
+    g = torch.Generator().manual_seed(31)
+    layers, rows, heads, dim = 3, 40, 2, 8
+    fill = torch.randn(2, layers, rows, heads, dim, generator=g).to(dtype)
+    pool = oi.RowStorePool(layers, rows, heads, dim, dtype=dtype, start_layer=2, fill=fill)
+    before_k = [b.clone() for b in pool.k_buffer]
+    before_v = [b.clone() for b in pool.v_buffer]
+    loc = torch.randperm(rows, generator=g)[:11]
+    k = torch.randn(11, heads, dim, generator=g, dtype=torch.float32)
+    v = torch.randn(11, heads, dim, generator=g, dtype=torch.float32)
+    for index in (loc, loc.to(torch.int32)):
+        pool.set_kv_buffer(None, index, k, v, layer_id_override=3)
+        assert torch.equal(pool._get_key_buffer(3)[loc.long()], k.to(dtype))
+        assert torch.equal(pool._get_value_buffer(3)[loc.long()], v.to(dtype))
+        rest = torch.ones(rows, dtype=torch.bool)
+        rest[loc.long()] = False
+        for i in range(layers):
+            kb, vb = pool.k_buffer[i], pool.v_buffer[i]
+            if i == 1:  # layer 3 (start_layer 2): only the rows at loc changed
+                assert torch.equal(kb[rest], before_k[i][rest]) and torch.equal(vb[rest], before_v[i][rest])
+            else:
+                assert torch.equal(kb, before_k[i]) and torch.equal(vb, before_v[i])
+    # A duplicate-free loc in the pool dtype is stored bit for bit.
+    k2 = torch.randn(11, heads, dim, generator=g).to(dtype)
+    pool.set_kv_buffer(None, loc, k2, k2, layer_id_override=2)
+    assert torch.equal(pool._get_key_buffer(2)[loc], k2)
+    assert torch.equal(pool._get_value_buffer(2)[loc], k2)
