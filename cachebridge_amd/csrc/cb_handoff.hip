@@ -1021,93 +1021,133 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
 }
 
 // ---------------------------------------------------------------------------
-// Support kernel (support s > 1, head_dim 128, bf16 K/V): a blocked GEMM with
-// producer and consumer waves.
+// Support kernel (support s > 1, head_dim 128, bf16 K/V).
 //
-// A target job's feature row is the concatenation of its s source rows, so
-// each job is a [T x s*128] . [s*128 x 128] contraction (the shipped top-8
-// recipe: 1024 input dims). An item is one 256-token block of one job. Its
-// input dims stream through LDS one k-step (32 dims) per stage, 4*s stages:
-// for q = 0, 1 and each support member k, k-step q (32 first-half dims)
-// then k-step q + 2 (their RoPE partners).
+// A target job's feature row is the concatenation of its s source rows, so a
+// job is a [T x s*128] . [s*128 x 128] contraction. An item is one 256-token
+// block of one job; the 8 waves of the (persistent, one per CU) workgroup
+// work on the same item, wave w on its tokens 32w .. 32w + 31, and each wave
+// computes all 128 outputs of its tokens with v_mfma_f32_32x32x16_bf16 into
+// 64 accumulator VGPRs (four 32-row tiles).
 //
-// One persistent workgroup of 8 waves per CU, a ring of four stage buffers
-// (the input of one k-step: 256 tokens x 32 dims x 2 terms, 32 KB):
-//   - producer waves 4..7 work on k-step pairs {q, q + 2} of one member:
-//     with the pair's source dims in registers (requested one pair ahead),
-//     they un-rotate keys and split both halves into bf16 terms, write the
-//     first stage as soon as its buffer is free and signal, hold the second
-//     stage's terms in registers until the next buffer is free, write and
-//     signal it;
-//   - consumer wave (h, c) loads the W fragments of its row tiles {h*2 + q',
-//     +4} (an output half with its RoPE partners; 2 terms, 8 KB per stage)
-//     straight from memory into registers one stage ahead (the workgroups of
-//     an XCD share each job's W in L2), waits until all four producers have
-//     signalled a stage, multiplies by column tiles 8c .. 8c + 7 (128
-//     tokens) into 128 accumulator VGPRs, releases the buffer, and after an
-//     item's last stage runs the epilogue (bias as the first accumulator
-//     input, target RoPE, cast, stores of whole 64-byte chunks of the target
-//     rows). Keeping W out of the producers shortens their per-pair work,
-//     which bounds the kernel, and leaves LDS room for a fourth stage.
-// Full and empty are monotonic per-buffer counters in LDS (each of the four
-// producer waves adds 1 when its part of a stage is written, each consumer
-// wave adds 1 when its reads of the stage are done), so no workgroup barrier
-// is needed after start-up and the loads in flight are never drained. LDS
-// executes one wave's operations in order, so data written before a counter
-// update is visible to a wave that has seen the update. Every wait is
-// bounded: after about a third of a second without progress a wave flags the
-// error word and sets a workgroup abort flag that ends every other wait, so
-// no launch can hang.
+// Stages: the item's input dims stream in 32-dim k-steps ks of each support
+// member k, in pairs (k-step q, then its RoPE partners q + 2), q = 0 for every
+// member, then q = 1: 4 s stages per item. Members are visited in ascending
+// (source layer, head) order.
 //
-// Items: the jobs of each window class are dealt to the 8 XCDs round-robin
-// (job j of a class to XCD j % 8, keys and values alike), each XCD's items
-// are its jobs' blocks in order, and the workgroups of an XCD take every
-// (workgroups per XCD)-th item of that list. The workgroups of one XCD then
-// run the blocks of one or two jobs at a time and read their W (512 KB at
-// s = 8) from their shared L2, and every XCD gets the same key/value mix.
-// W is packed with the group output permutation (grp_out_dim).
+// Memory traffic of the stage loop is LDS DMA only (global_load_lds_dwordx4,
+// nothing staged in registers), waited for with explicit counts:
+//   - each stage's split W (four row tiles x two 16-dim MFMA k-steps x two
+//     bf16 terms, 16 KB) goes into a four-slot LDS ring three stages ahead,
+//     one workgroup barrier per stage publishing the stage after next and
+//     freeing the slot just used;
+//   - each wave's source rows of a k-step pair (its 32 tokens x 64 bytes,
+//     and their RoPE partners) go into its own two-buffer LDS area two
+//     stages ahead, 16 tokens x one 64-byte sector per instruction.
+// Without these two distances the gathers' latency, not the MFMAs, set the
+// kernel's pace: the scattered 64-byte sectors of the token rows mostly come
+// from beyond L2.
+//
+// Every wave produces its own input: the split bf16 terms of the next k-step
+// pair are built (keys un-rotated, split) from its LDS rows while the current
+// pair's MFMAs run, half of them in each of the pair's two stages. On gfx950
+// an MFMA leaves its own wave free to issue other instructions while it
+// executes, but a second wave's VALU work on the same SIMD does not overlap
+// another wave's MFMAs; keeping the conversion inside the MFMA wave's
+// instruction stream is what lets it hide.
+//
+// Items go to XCDs in runs of adjacent jobs (SupItems below), so that the
+// items running on one XCD at a time share source rows in its L2.
+//
+// Lane layout (lane l: token n = l % 32 of the wave, half h = l / 32):
+//   input: MFMA k-step kk of 32-dim k-step ks covers member dims
+//          32 ks + 16 h + 8 kk + e (e = 0..7) in lane half h, so a lane
+//          reads 32 contiguous bytes of its token's row per k-step and its
+//          RoPE partners (ks + 2) sit in the same lane;
+//   output: row r = 8v + 4h' + u of row tile t is output dim
+//          64 (t >> 1) + 32 (t & 1) + 16 (v >> 1) + 8 h' + 4 (v & 1) + u; the
+//          accumulator register 4v + u of lane (n, h) holds row 8v + 4h + u,
+//          so tiles t and t + 2 hold RoPE partners in the same register and a
+//          lane's outputs are runs of 8 dims (16-byte stores).
+// W is packed [job][stage][kk][row tile][term][lane][8 bf16] in the order the
+// stages are consumed: stage i covers pair p = i / 2 (k-step half q = p / S,
+// member p % S) at 32-dim k-step q + 2 (i & 1).
 // ---------------------------------------------------------------------------
 
-constexpr int kSupTile = 256;                 // tokens per item
-constexpr int kSupWaves = 8;                  // 4 consumer and 4 producer waves
-constexpr int kSupThreads = kSupWaves * kWave;
-constexpr int kSupRoleWaves = 4;
-constexpr int kSupRing = 4;
+// s_waitcnt immediates (vmcnt in bits 3:0, expcnt 6:4, lgkmcnt 11:8; the
+// other counters left at their maximum, i.e. not waited for).
+constexpr int kVmcnt0 = 0x0f70;
+constexpr int kVmcnt2 = 0x0f72;
+constexpr int kVmcnt6 = 0x0f76;
 
-// Output dim of row r (0..15) of row tile rt (0..7): tile rt = p*4 + h*2 + q
-// holds in lane group g = r / 4 the dims p*64 + h*32 + g*8 + q*4 + r % 4, so
-// the wave that owns half h (tiles h*2 + q and their RoPE partners, +4) has 8
-// consecutive dims in each lane group and each store instruction writes
-// whole 64-byte chunks of a target row.
-__host__ __device__ inline int grp_out_dim(int rt, int r) {
-  return (rt >> 2) * 64 + ((rt >> 1) & 1) * 32 + (r >> 2) * 8 + (rt & 1) * 4 + (r & 3);
+constexpr int kSupTile = 256;                  // tokens per item
+constexpr int kSupWaves = 8;
+constexpr int kSupThreads = kSupWaves * kWave;
+constexpr int kSupStageU4 = 4 * 2 * 2 * kWave;  // uint4 per stage (16 KB)
+
+__host__ __device__ inline int sup_out_dim(int t, int r) {
+  const int v = r >> 3, h = (r >> 2) & 1, u = r & 3;
+  return 64 * (t >> 1) + 32 * (t & 1) + 16 * (v >> 1) + 8 * h + 4 * (v & 1) + u;
+}
+__host__ __device__ inline int sup_in_dim(int ks, int kk, int h, int e) { return 32 * ks + 16 * h + 8 * kk + e; }
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ inline f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// One stage buffer: the input [column tile][term][lane] of one k-step (32 KB).
-struct SupStage {
-  uint4 x[16][2][kWave];
-};
+__global__ void pack_support_kernel(const float* __restrict__ w, const float* __restrict__ bias,
+                                     const int32_t* __restrict__ order, const int32_t* __restrict__ mperm,
+                                     int njobs, int S, uint16_t* __restrict__ wp, float* __restrict__ bp) {
+  constexpr int D = 128;
+  const int64_t per_member = static_cast<int64_t>(kSupStageU4) * 4 * 8;  // bf16 values: 4 ks x 16 KB
+  const int64_t total = per_member * S * njobs;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int64_t rem = idx;
+    const int e = rem % 8; rem /= 8;
+    const int lane = rem % kWave; rem /= kWave;
+    const int term = rem % 2; rem /= 2;
+    const int t = rem % 4; rem /= 4;
+    const int kk = rem % 2; rem /= 2;
+    const int i = rem % (4 * S); rem /= 4 * S;  // stage of the item
+    const int pr = i >> 1, q = pr >= S ? 1 : 0, k = pr - q * S, ks = q + 2 * (i & 1);
+    const int j = static_cast<int>(rem);
+    const int fo = sup_out_dim(t, lane & 31);
+    const int fi = mperm[static_cast<int64_t>(order[j]) * S + k] * D + sup_in_dim(ks, kk, lane >> 5, e);
+    float r = w[(static_cast<int64_t>(order[j]) * S * D + fi) * D + fo];
+    uint16_t hb = 0;
+    for (int tt = 0; tt <= term; ++tt) {
+      hb = f2bf(r);
+      r = r - bf2f(hb);
+    }
+    wp[idx] = hb;
+  }
+  const int64_t nb = static_cast<int64_t>(njobs) * D;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < nb;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int j = static_cast<int>(idx / D);
+    bp[idx] = bias[static_cast<int64_t>(order[j]) * D + idx % D];
+  }
+}
 
-struct SupShared {
-  SupStage ring[kSupRing];
-  int32_t trow[2][kSupTile];  // [item parity]: target row per token (-1: write nothing)
-  int32_t tpos[2][kSupTile];  // [item parity]: target position per token
-  float bias[2][128];         // [item parity]
-  uint32_t full[kSupRing];    // producer-wave fills of each buffer
-  uint32_t empty[kSupRing];   // consumer-wave releases of each buffer
-  uint32_t abort;             // set when a wait timed out
-};
-
-// The items of workgroup (x, y): see the header comment.
+// Items of the support kernel: XCD x takes units x, x + 8, ... of each class
+// (the plan orders the units so that these are a run of adjacent keys jobs
+// and a run of adjacent values jobs in the sorted job order, whose support
+// lists share source layers) and runs them in groups of kSupJobGroup jobs,
+// the group's jobs interleaved per token chunk, so that the items an XCD
+// runs at one time read overlapping source rows and share its L2.
+constexpr int kSupJobGroup = 16;
 struct SupItems {
-  int x, y, nwg;
+  int x, nwg;
   int64_t next;  // position in XCD x's item list
 
   struct Item {
     int job, lo, hi;
   };
 
-  __device__ bool get(const MapArgs& a, Item& it) const {
+  __device__ __attribute__((always_inline)) bool get(const MapArgs& a, SupItems::Item& it) const {
     int64_t p = next;
     for (int c = 0; c < a.ncls; ++c) {
       const int nj = a.cls_unit_end[c] - a.cls_unit_begin[c];
@@ -1115,9 +1155,13 @@ struct SupItems {
       const int nch = a.cls_nchunks[c];
       const int64_t count = static_cast<int64_t>(mine) * nch;
       if (p < count) {
-        const int jl = static_cast<int>(p / nch), bk = static_cast<int>(p - static_cast<int64_t>(jl) * nch);
+        const int64_t gsz = static_cast<int64_t>(kSupJobGroup) * nch;
+        const int g = static_cast<int>(p / gsz);
+        const int r = static_cast<int>(p - g * gsz);
+        const int gj = min(kSupJobGroup, mine - g * kSupJobGroup);
+        const int ch = r / gj, jl = g * kSupJobGroup + (r - ch * gj);
         it.job = cload(a.unit_job + a.cls_unit_begin[c] + x + 8 * jl);
-        it.lo = a.cls_tok_first[c] + bk * kSupTile;
+        it.lo = a.cls_tok_first[c] + ch * kSupTile;
         it.hi = min(it.lo + kSupTile, a.cls_tok_first[c] + a.cls_tok_count[c]);
         return true;
       }
@@ -1127,408 +1171,388 @@ struct SupItems {
   }
 };
 
-__device__ inline CB_LDS uint32_t* lds_u32(uint32_t* p) { return (CB_LDS uint32_t*)p; }
-
-// Wait until *ctr >= target (or the workgroup aborted). Bounded: about 2^22
-// polls of at least 64 clocks each.
-__device__ inline void sup_wait(SupShared& S, uint32_t* ctr, uint32_t target, int* err) {
-  volatile CB_LDS uint32_t* c = lds_u32(ctr);
-  volatile CB_LDS uint32_t* ab = lds_u32(&S.abort);
-  for (int i = 0; i < (1 << 22); ++i) {
-    const uint32_t v = __builtin_amdgcn_readfirstlane(*c);
-    if (v >= target || __builtin_amdgcn_readfirstlane(*ab)) {
-      asm volatile("" ::: "memory");
-      return;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-  if ((threadIdx.x & (kWave - 1)) == 0) {
-    atomicOr(err, 4);
-    *ab = 1;
-  }
-  asm volatile("" ::: "memory");
-}
-
-// Add 1 to *ctr once the wave's earlier LDS operations are done.
-__device__ inline void sup_signal(uint32_t* ctr) {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  if ((threadIdx.x & (kWave - 1)) == 0)
-    __hip_atomic_fetch_add(lds_u32(ctr), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// Producer's view of an item: what its loads and its LDS side tables need.
-struct SupLoad {
-  bool valid, is_k;
-  int npair;            // k-step pairs of the item: 2 * support
-  int pjv;              // lane k < support: the job's support pair k
-  int kind;
-  int64_t soff[4];      // per task: source row byte offset, -1 for the zero row
-  int pos[4];           // per task: source position
+// One wave's view of an item: its token's rows and position, the job's maps
+// and tables.
+struct SupLane {
+  int job, kind, lo, hi;
+  bool live;          // this lane's token is inside the item
+  int64_t soff;       // source row byte offset (-1: the zero row)
+  int32_t trow;       // target row (-1: write nothing)
+  int pos;            // position of this lane's token
   const CB_GLOBAL float* ucos;
   const CB_GLOBAL float* usin;
 };
 
-// Producer thread (wave pw, lane): tasks j = 0..3 are column tile 4 * pw + j,
-// token 16 * (4 * pw + j) + (lane & 15), first-half dims 16g + 8q .. +7
-// (g = lane >> 4) and their partners.
-__device__ inline void sup_decode(const MapArgs& a, SupShared& S, const SupItems::Item& it, int parity,
-                                  int pw, SupLoad& L) {
-  constexpr int D = 128;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int g = lane >> 4, col = lane & 15;
-  const int* jm = reinterpret_cast<const int*>(a.jobs + it.job);
-  const int meta_y = cload(jm + 1), meta_z = cload(jm + 2);
-  L.valid = true;
-  L.kind = meta_y & 0xff;
-  L.is_k = L.kind == CB_KIND_K;
-  L.npair = 2 * a.support;
-  // One vector load per item, waited for with the item's row indices below;
-  // each k-step pair then picks its pair with readlane instead of a scalar
-  // load whose latency would stall every pair.
-  L.pjv = lane < a.support
-              ? reinterpret_cast<const CB_GLOBAL int32_t*>(as_global(a.pairs))[static_cast<size_t>(it.job) * a.support + lane]
-              : 0;
-  const int sth = (meta_y >> 16) & 0xff;
-  const bool shared = (meta_z & kJobSharedTables) != 0;
-  L.ucos = gtab(shared ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
-  L.usin = gtab(shared ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
-  const int n = it.hi - it.lo;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pt = 16 * (4 * pw + j) + col;
-    const int tk = it.lo + min(pt, n - 1);
-    const bool live = pt < n;
-    const int64_t srow = row_of(a.src, tk);
-    const int64_t drow = row_of(a.tgt, tk);
-    const bool sok = srow >= 0 && srow < a.src.rows;
-    const bool dok = drow >= 0 && drow < a.tgt.rows;
-    if (live && !(sok && dok) && g == 0) atomicOr(a.err, (sok ? 0 : 1) | (dok ? 0 : 2));
-    L.soff[j] = live && sok ? srow * a.src.row_stride_b : -1;
-    L.pos[j] = position_of(a, tk);
-    if (g == 0) {
-      // A token whose source row is out of range writes nothing.
-      S.trow[parity][pt] = live && sok && dok ? static_cast<int32_t>(drow) : -1;
-      S.tpos[parity][pt] = L.pos[j];
-    }
-  }
-  const int pt = (threadIdx.x - kSupRoleWaves * kWave);
-  if (pt < D) S.bias[parity][pt] = a.bias[static_cast<size_t>(it.job) * D + pt];
-}
-
-// Source dims of k-step pair t for the four tasks: 8 first-half dims and
-// their partners each.
-__device__ inline void sup_issue_x(const MapArgs& a, const SupLoad& L, int t, uint4 (&x)[4][2]) {
-  constexpr int HALF = 64;
-  const int S = a.support;
-  const int g = (threadIdx.x & (kWave - 1)) >> 4;
-  const int q = t >= S ? 1 : 0, k = t - q * S;
-  const int pr = __builtin_amdgcn_readlane(L.pjv, k);
-  gcptr base = layer_base(a.src, L.kind, pr & 0xffff) + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * 128 * 2;
-  gcptr zrow = as_global(a.zero);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    gcptr p = (L.soff[j] >= 0 ? base + L.soff[j] : zrow) + (16 * g + 8 * q) * 2;
-    x[j][0] = gload<uint4>(p);
-    x[j][1] = gload<uint4>(p + HALF * 2);
-  }
-}
-
-// Un-rotation values of the four tasks of item L for k-step pair q.
-__device__ inline void sup_issue_tab(const SupLoad& L, int q, float (&c)[4][8], float (&s)[4][8]) {
-  const int g = (threadIdx.x & (kWave - 1)) >> 4;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t off = tab_chunk<16>(L.pos[j], 2 * q + u, g);
-      const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(L.ucos + off);
-      const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(L.usin + off);
-      c[j][4 * u] = c4.x; c[j][4 * u + 1] = c4.y; c[j][4 * u + 2] = c4.z; c[j][4 * u + 3] = c4.w;
-      s[j][4 * u] = s4.x; s[j][4 * u + 1] = s4.y; s[j][4 * u + 2] = s4.z; s[j][4 * u + 3] = s4.w;
-    }
-}
-
-// Producer side of the whole launch (waves 4..7). L is the item of the
-// loads, which run one k-step pair ahead of the production (and so move to
-// the next item one pair before the producing item ends).
-__device__ void sup_producer(const MapArgs& a, SupShared& S, SupItems items) {
+template <bool IS_K>
+__device__ __attribute__((always_inline)) void support_item(const MapArgs& a, uint4* lds, uint4* xa, uint4* xb,
+                                                         const SupLane& I, int wave, uint32_t& slot) {
 #pragma clang fp contract(off)
+  constexpr int D = 128;
+  constexpr int XT = IS_K ? 2 : 1;          // input terms
   const int lane = threadIdx.x & (kWave - 1);
-  const int pw = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) - kSupRoleWaves;
-  const int Sup = a.support;
-  const int npair = 2 * Sup;
-  SupItems::Item it;
-  if (!items.get(a, it)) return;
-  SupLoad L;
-  int load_parity = 0;
-  sup_decode(a, S, it, 0, pw, L);
-  uint4 x[4][2];
-  float tc[4][8], ts[4][8];
-  if (L.is_k) sup_issue_tab(L, 0, tc, ts);
-  sup_issue_x(a, L, 0, x);
-  int lt = 1;       // pair of L the next loads are for
-  uint32_t n = 0;   // global stage index
-  bool p_is_k = L.is_k;
+  const int h = lane >> 5;
+  const int S = a.support;
+  const int npair = 2 * S;                   // (q, member) pairs; two stages each
+  const int* jm = reinterpret_cast<const int*>(a.jobs + I.job);
+  const int mx = cload(jm), meta_y = cload(jm + 1);
+  const int tth = (meta_y >> 24) & 0xff;
 
-  // Moves the loads to the next pair (and L to the next item at its end).
-  bool next_valid = true;
-  int next_t = 0;
-  auto advance = [&]() {
-    if (!L.valid) {
-      next_valid = false;
-      return;
+  // W stages of the job, 16 KB each, packed in the order they are consumed.
+  gcptr wjob = as_global(a.w + static_cast<size_t>(I.job) * S * 4 * kSupStageU4);
+  const int nst = 4 * S;
+  // Lane j < 2S holds the address of pair j's source head (its layer's base,
+  // the head and the k-step half q = j / S) for the row requests, which read
+  // it with readlane: no scalar loads (and their waits) in the stage loop.
+  // A token without a source row (outside the item, or a row out of range)
+  // reads row 0 instead (pools have at least one row): it writes only to the
+  // sink, and a token's products touch only its own outputs.
+  uint64_t pbase;
+  {
+    const int j = min(lane, npair - 1);
+    const int q = j >= S ? 1 : 0, k = j - q * S;
+    const int pr = *(reinterpret_cast<const CB_GLOBAL int*>(as_global(a.pairs)) + static_cast<size_t>(I.job) * S + k);
+    const int layer = pr & 0xffff;
+    const void* const* arr = I.kind ? a.src.v_layers : a.src.k_layers;
+    gcptr lb = arr ? *(reinterpret_cast<const gcptr CB_GLOBAL*>(as_global(arr)) + layer)
+                   : as_global(I.kind ? a.src.v_base : a.src.k_base) + layer * a.src.layer_stride_b;
+    pbase = reinterpret_cast<uint64_t>(lb + static_cast<int64_t>((pr >> 16) - a.src.head_offset) * D * 2 + 64 * q);
+  }
+  const uint32_t pb_lo = static_cast<uint32_t>(pbase), pb_hi = static_cast<uint32_t>(pbase >> 32);
+  // Accumulators start at the bias: register 4v + u of tile t holds output
+  // dim sup_out_dim(t, 8v + 4h + u).
+  f32x16 acc[4];
+  {
+    const CB_GLOBAL float* bj = reinterpret_cast<const CB_GLOBAL float*>(as_global(a.bias)) + static_cast<size_t>(I.job) * D;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int base = 64 * (t >> 1) + 32 * (t & 1) + 8 * h;
+      const float4 b0 = *reinterpret_cast<const CB_GLOBAL float4*>(bj + base);
+      const float4 b1 = *reinterpret_cast<const CB_GLOBAL float4*>(bj + base + 4);
+      const float4 b2 = *reinterpret_cast<const CB_GLOBAL float4*>(bj + base + 16);
+      const float4 b3 = *reinterpret_cast<const CB_GLOBAL float4*>(bj + base + 20);
+      acc[t] = f32x16{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w,
+                      b2.x, b2.y, b2.z, b2.w, b3.x, b3.y, b3.z, b3.w};
     }
-    if (lt == npair) {
-      items.next += items.nwg;
-      if (!items.get(a, it)) {
-        L.valid = false;
-        next_valid = false;
-        return;
-      }
-      load_parity ^= 1;
-      sup_decode(a, S, it, load_parity, pw, L);
-      lt = 0;
+  }
+
+  // Un-rotation values (keys) of k-step q for this lane's 16 dims
+  // 32q + 16h + 8kk + e: table group g = 2q + h, value groups 2kk, 2kk + 1.
+  float tc[2][8], ts[2][8];
+  auto load_tab_q = [&](int q) __attribute__((always_inline)) {
+    if constexpr (IS_K) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t off = tab_chunk<16>(I.pos, 2 * kk + u, 2 * q + h);
+          const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(I.ucos + off);
+          const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(I.usin + off);
+          float* c = tc[kk] + 4 * u;
+          float* sn = ts[kk] + 4 * u;
+          c[0] = c4.x; c[1] = c4.y; c[2] = c4.z; c[3] = c4.w;
+          sn[0] = s4.x; sn[1] = s4.y; sn[2] = s4.z; sn[3] = s4.w;
+        }
     }
-    next_t = lt;
-    ++lt;
   };
 
-  SupItems prod = items;  // the producing item (behind L by at most one)
-  for (;;) {
-    for (int t = 0; t < npair; ++t) {
-      // Both stages' input terms of this pair, from x (and the un-rotation
-      // values of its q, requested one pair ahead).
-      uint4 xa[4][2], xb[4][2];  // [task][term]: first stage (q), second stage (q + 2)
+  // Fragments of a k-step pair: [stage of the pair][kk][term][element pair]
+  // (dword c of a fragment holds dims 2c, 2c + 1 of its 8). The current
+  // pair's are read by the MFMAs while the next pair's are built, in two
+  // buffers that swap roles every pair (the pair loop is unrolled by two,
+  // so the roles are compile-time).
+  typedef uint32_t Frags[2][2][XT][4];
+  Frags fa, fb;
+
+  // Memory traffic of the stage loop is LDS DMA only, issued from inline
+  // assembly and waited for with explicit counts (the compiler, unaware of
+  // it, adds no waits of its own). In issue order, stage i of the item
+  // requests W stage i + 3 (2 instructions), then in the first stage of a
+  // pair the source rows of the pair after next (4 instructions); both
+  // complete in issue order.
+  //
+  // W ring: four 16 KB slots, stage j in slot (s0 + j) % 4. W stage i + 3
+  // goes into the slot stage i - 1 used (free after the barrier that opens
+  // stage i) and must have landed before the barrier that opens stage i + 2
+  // (its first reads, a step ahead, are in stage i + 2's last step):
+  // before opening stage i + 1 a wave waits until at most 6 of its DMA
+  // instructions are outstanding, which leaves only those issued after
+  // W stage i + 2.
+  //
+  // Source rows: pair k's go to buffer k & 1 of the wave (4 KB), two stages
+  // before its fragments are built (in pair k - 1); the buffer was last read
+  // in pair k - 2. DMA instruction r = 2 part + tg covers 16 tokens x 64
+  // bytes (part 0: dims 32q..32q+31, part 1: their partners; tg: tokens
+  // 16 tg..16 tg+15): DMA lane L loads 16-byte chunk (L & 3) ^ ((L >> 4) & 3)
+  // of token L >> 2, so each 4-lane quad reads one 64-byte sector and the
+  // readers' 16-lane groups hit distinct banks. Before the first read of
+  // pair k's rows (start of pair k - 1) at most 2 DMA instructions (the W
+  // stage requested since) may be outstanding.
+  auto dma16 = [&](gcptr src, const uint4* dst) __attribute__((always_inline)) {
+    const uint32_t la = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((CB_LDS const uint4*)dst)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(reinterpret_cast<uint64_t>(src)), "s"(la) : "memory", "m0");
+  };
+  auto w_dma = [&](int j, uint32_t sl) __attribute__((always_inline)) {
+    gcptr src = wjob + static_cast<int64_t>(min(j, nst - 1)) * (kSupStageU4 * 16) + (wave * 128 + lane) * 16;
+    const uint4* dst = lds + sl * kSupStageU4 + wave * 128;
+    dma16(src, dst);
+    dma16(src + kWave * 16, dst + kWave);
+  };
+  uint64_t doff[2];
+  {
+    const int c = (lane & 3) ^ ((lane >> 4) & 3);
+    const uint64_t mine = static_cast<uint64_t>(I.soff < 0 ? 0 : I.soff);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (p_is_k) {
-          float x1[8], x2[8];
-          unpack16<uint16_t>(x[j][0], x1);
-          unpack16<uint16_t>(x[j][1], x2);
+    for (int tg = 0; tg < 2; ++tg) {
+      const int from = (16 * tg + (lane >> 2)) * 4;
+      const uint32_t lo = __builtin_amdgcn_ds_bpermute(from, static_cast<int>(static_cast<uint32_t>(mine)));
+      const uint32_t hi = __builtin_amdgcn_ds_bpermute(from, static_cast<int>(static_cast<uint32_t>(mine >> 32)));
+      doff[tg] = ((static_cast<uint64_t>(hi) << 32) | lo) + 16 * c;
+    }
+  }
+  auto src_dma = [&](int p, uint4* X) __attribute__((always_inline)) {
+    const int pp = min(p, npair - 1);
+    const uint64_t b = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(pb_hi, pp))) << 32) |
+                       static_cast<uint32_t>(__builtin_amdgcn_readlane(pb_lo, pp));
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float k1 = __builtin_fmaf(x1[e], tc[j][e], x2[e] * ts[j][e]);
-            const float k2 = __builtin_fmaf(x2[e], tc[j][e], -(x1[e] * ts[j][e]));
-            x1[e] = k1;
-            x2[e] = k2;
-          }
-          uint32_t t1[2][4], t2[2][4];
-          split_terms<2, 8>(x1, t1);
-          split_terms<2, 8>(x2, t2);
+    for (int r = 0; r < 4; ++r)
+      dma16(reinterpret_cast<gcptr>(b + doff[r & 1] + 128 * (r >> 1)), X + wave * 256 + r * 64);
+  };
+  uint4 raw[2];  // first-half dims and partners of one kk half, this lane's 8 each
+  const int xn16 = lane & 15, xtg = (lane >> 4) & 1;
+  auto read_raw = [&](int kk, const uint4* X) __attribute__((always_inline)) {
+    const int cc = (2 * h + kk) ^ (xn16 >> 2);
+    raw[0] = X[wave * 256 + xtg * 64 + 4 * xn16 + cc];
+    raw[1] = X[wave * 256 + (2 + xtg) * 64 + 4 * xn16 + cc];
+  };
+  // Element pair c (dims 2c, 2c + 1 of the 8) of the kk half held in raw:
+  // keys un-rotated and split into two bf16 terms, values copied.
+  auto produce = [&](Frags& nx, int kk, int c) __attribute__((always_inline)) {
+    const uint32_t w1 = c == 0 ? raw[0].x : c == 1 ? raw[0].y : c == 2 ? raw[0].z : raw[0].w;
+    const uint32_t w2 = c == 0 ? raw[1].x : c == 1 ? raw[1].y : c == 2 ? raw[1].z : raw[1].w;
+    if constexpr (IS_K) {
+      const float a1 = lo_bf(w1), b1 = hi_bf(w1), a2 = lo_bf(w2), b2 = hi_bf(w2);
+      const float c0 = tc[kk][2 * c], c1 = tc[kk][2 * c + 1], s0 = ts[kk][2 * c], s1 = ts[kk][2 * c + 1];
+      const float k1a = __builtin_fmaf(a1, c0, a2 * s0), k1b = __builtin_fmaf(b1, c1, b2 * s1);
+      const float k2a = __builtin_fmaf(a2, c0, -(a1 * s0)), k2b = __builtin_fmaf(b2, c1, -(b1 * s1));
+      const uint32_t h1 = pack_bf16(k1a, k1b), h2 = pack_bf16(k2a, k2b);
+      nx[0][kk][0][c] = h1;
+      nx[0][kk][1][c] = pack_bf16(k1a - lo_bf(h1), k1b - hi_bf(h1));
+      nx[1][kk][0][c] = h2;
+      nx[1][kk][1][c] = pack_bf16(k2a - lo_bf(h2), k2b - hi_bf(h2));
+      // Keep the work in this step (next to this step's products) rather
+      // than sunk toward the pair's end, where its results are first read.
+      asm volatile("" :: "v"(nx[0][kk][0][c]), "v"(nx[0][kk][1][c]), "v"(nx[1][kk][0][c]), "v"(nx[1][kk][1][c]));
+    } else {
+      nx[0][kk][0][c] = w1;
+      nx[1][kk][0][c] = w2;
+    }
+  };
+  auto frag = [&](const uint32_t (&f)[4]) __attribute__((always_inline)) {
+    return __builtin_bit_cast(bf16x8, make_uint4(f[0], f[1], f[2], f[3]));
+  };
+  auto ring = [](uint32_t sl, int d) __attribute__((always_inline)) { return (sl + d) & 3u; };
+
+  // Prologue: W stages 0-2 into the three slots after the previous item's
+  // last one (that slot may still be read by other waves; the other three
+  // were last read before the barrier that opened the previous item's last
+  // stage) and the first two pairs' rows; everything this wave has in
+  // flight (including the previous item's stores) is waited for, then the
+  // barrier publishes W, and the first pair's fragments are built.
+  const uint32_t s0 = ring(slot, 1);
+  load_tab_q(0);
+  w_dma(0, s0);
+  w_dma(1, ring(s0, 1));
+  w_dma(2, ring(s0, 2));
+  src_dma(0, xa);
+  src_dma(1, xb);
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  asm volatile("s_barrier" ::: "memory");
 #pragma unroll
-          for (int v = 0; v < 2; ++v) {
-            xa[j][v] = make_uint4(t1[v][0], t1[v][1], t1[v][2], t1[v][3]);
-            xb[j][v] = make_uint4(t2[v][0], t2[v][1], t2[v][2], t2[v][3]);
-          }
+  for (int kk = 0; kk < 2; ++kk) {
+    read_raw(kk, xa);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) produce(fa, kk, c);
+  }
+  if (IS_K && S == 1) {
+    load_tab_q(1);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  }
+  slot = s0;  // slot of the current stage
+
+  // W fragments [ring][tile 0/1 of the step's pair][term], read a step ahead.
+  bf16x8 wf[2][4];
+  auto read_w = [&](uint32_t sl, int step, bf16x8 (&dst)[4]) __attribute__((always_inline)) {
+    const uint4* ws = lds + sl * kSupStageU4;
+    const int kk = step >> 1, tp = step & 1;
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+      dst[f] = __builtin_bit_cast(bf16x8, ws[((kk * 4 + 2 * tp + (f >> 1)) * 2 + (f & 1)) * kWave + lane]);
+  };
+  read_w(slot, 0, wf[0]);
+
+  // One k-step pair: stages 2p (k-step q) and 2p + 1 (q + 2) with the
+  // fragments in cur, building the next pair's (rows in buffer xr) into
+  // nxt; the pair after next's rows go to buffer xw. Steps (kk, tile pair
+  // tp) of a stage run that step's products of tiles 2tp and 2tp + 1
+  // alternately, with element pair `step` of the next pair's kk = half
+  // half produced beside them.
+  auto pair = [&](int p, Frags& cur, Frags& nxt, const uint4* xr, uint4* xw) __attribute__((always_inline)) {
+    if (IS_K && p + 1 == S && S > 1) {  // the next pair starts q = 1
+      // Waited for here, once per item, so that no later wait (which would
+      // also drain the DMA in flight) is needed for them.
+      load_tab_q(1);
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int i = 2 * p + half;  // stage of the item
+      if (half == 0) {
+        __builtin_amdgcn_s_waitcnt(kVmcnt2);  // pair p + 1's rows
+        asm volatile("" ::: "memory");
+      }
+      read_raw(half, xr);
+      w_dma(i + 3, ring(slot, 3));
+      if (half == 0) src_dma(p + 2, xw);
+      const uint32_t nsl = ring(slot, 1);
+#pragma unroll
+      for (int step = 0; step < 4; ++step) {
+        if (step < 3) read_w(slot, step + 1, wf[(step + 1) & 1]);
+        else read_w(nsl, 0, wf[0]);
+        const int kk = step >> 1, t0 = 2 * (step & 1);
+        const bf16x8* w = wf[step & 1];  // {t0 term0, t0 term1, t1 term0, t1 term1}
+        const bf16x8 x0 = frag(cur[half][kk][0]);
+        if constexpr (IS_K) {
+          const bf16x8 x1 = frag(cur[half][kk][XT - 1]);
+          acc[t0] = mfma32(w[1], x0, acc[t0]);
+          acc[t0 + 1] = mfma32(w[3], x0, acc[t0 + 1]);
+          acc[t0] = mfma32(w[0], x1, acc[t0]);
+          acc[t0 + 1] = mfma32(w[2], x1, acc[t0 + 1]);
+          acc[t0] = mfma32(w[0], x0, acc[t0]);
+          acc[t0 + 1] = mfma32(w[2], x0, acc[t0 + 1]);
         } else {
-          xa[j][0] = x[j][0];
-          xb[j][0] = x[j][1];
-          xa[j][1] = xb[j][1] = make_uint4(0, 0, 0, 0);
+          acc[t0] = mfma32(w[1], x0, acc[t0]);
+          acc[t0 + 1] = mfma32(w[3], x0, acc[t0 + 1]);
+          acc[t0] = mfma32(w[0], x0, acc[t0]);
+          acc[t0 + 1] = mfma32(w[2], x0, acc[t0 + 1]);
         }
+        produce(nxt, half, step);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // The source and table registers are free: request the next pair's
-      // source dims, and its un-rotation values when its q starts (keys).
-      advance();
-      if (next_valid) sup_issue_x(a, L, next_t, x);
-      if (next_valid && L.is_k && (next_t == 0 || next_t == Sup)) sup_issue_tab(L, next_t == 0 ? 0 : 1, tc, ts);
-      // First stage (k-step q).
-      {
-        const int slot = n % kSupRing;
-        sup_wait(S, &S.empty[slot], 4 * (n / kSupRing), a.err);
-        SupStage& B = S.ring[slot];
+      // Close stage i: W stage i + 2 must have landed (at most 6 younger
+      // DMA instructions outstanding), then the barrier publishes it and
+      // frees stage i's slot.
+      __builtin_amdgcn_s_waitcnt(kVmcnt6);
+      asm volatile("s_barrier" ::: "memory");
+      slot = nsl;
+    }
+  };
+  for (int p = 0; p < npair; p += 2) {  // npair = 2 S is even
+    pair(p, fa, fb, xb, xa);
+    pair(p + 1, fb, fa, xa, xb);
+  }
+  // slot is now one past the item's last stage: step back to it.
+  slot = ring(slot, 3);
+
+  // Epilogue: target RoPE (keys), cast, store. Tile tt (0, 1) and its
+  // partner tt + 2; register 4v + u is first-half dim
+  // 32 tt + 16 (v >> 1) + 8h + 4 (v & 1) + u.
+  gptr tbase = const_cast<gptr>(layer_base(a.tgt, I.kind, mx & 0xffff)) +
+               static_cast<int64_t>((mx >> 16) - a.tgt.head_offset) * D * 2;
+  gptr dst = I.trow >= 0 ? tbase + static_cast<int64_t>(I.trow) * a.tgt.row_stride_b
+                         : as_global(a.sink) + lane * 512;
+  const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
+  const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          B.x[4 * pw + j][0][lane] = xa[j][0];
-          if (p_is_k) B.x[4 * pw + j][1][lane] = xa[j][1];
-        }
-        sup_signal(&S.full[slot]);
-        ++n;
-      }
-      // Second stage (k-step q + 2).
-      {
-        const int slot = n % kSupRing;
-        sup_wait(S, &S.empty[slot], 4 * (n / kSupRing), a.err);
-        SupStage& B = S.ring[slot];
+  for (int tt = 0; tt < 2; ++tt) {
+    float y1[16], y2[16];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          B.x[4 * pw + j][0][lane] = xb[j][0];
-          if (p_is_k) B.x[4 * pw + j][1][lane] = xb[j][1];
+    for (int r = 0; r < 16; ++r) {
+      y1[r] = acc[tt][r];
+      y2[r] = acc[tt + 2][r];
+    }
+    if constexpr (IS_K) {
+      float cv[16], sv[16];
+#pragma unroll
+      for (int vh = 0; vh < 2; ++vh)      // v >> 1: table group 2tt + vh
+#pragma unroll
+        for (int vl = 0; vl < 2; ++vl) {  // v & 1: value group 2h + vl
+          const int64_t off = tab_chunk<16>(I.pos, 2 * h + vl, 2 * tt + vh);
+          const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
+          const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
+          const int r0 = 4 * (2 * vh + vl);
+          cv[r0] = c4.x; cv[r0 + 1] = c4.y; cv[r0 + 2] = c4.z; cv[r0 + 3] = c4.w;
+          sv[r0] = s4.x; sv[r0 + 1] = s4.y; sv[r0 + 2] = s4.z; sv[r0 + 3] = s4.w;
         }
-        sup_signal(&S.full[slot]);
-        ++n;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float a1 = y1[r], a2 = y2[r];
+        y1[r] = __builtin_fmaf(a1, cv[r], -(a2 * sv[r]));
+        y2[r] = __builtin_fmaf(a2, cv[r], a1 * sv[r]);
       }
     }
-    prod.next += prod.nwg;
-    SupItems::Item pit;
-    if (!prod.get(a, pit)) break;
-    const int* jm = reinterpret_cast<const int*>(a.jobs + pit.job);
-    p_is_k = (cload(jm + 1) & 0xff) == CB_KIND_K;
-  }
-}
-
-// Consumer side of the whole launch (waves 0..3).
-__device__ void sup_consumer(const MapArgs& a, SupShared& S, SupItems items) {
-#pragma clang fp contract(off)
-  constexpr int D = 128, HALF = 64;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int g = lane >> 4, col = lane & 15;
-  const int hh = wave >> 1, cb = wave & 1;
-  const int Sup = a.support;
-  const int nstage = 4 * Sup;
-  gptr sink = as_global(a.sink) + lane * 512;
-  uint32_t n = 0;
-  int parity = 0;
-  SupItems::Item it;
-  for (; items.get(a, it); items.next += items.nwg, parity ^= 1) {
-    const int* jm = reinterpret_cast<const int*>(a.jobs + it.job);
-    const int mx = cload(jm), meta_y = cload(jm + 1);
-    const int kind = meta_y & 0xff;
-    const int tth = (meta_y >> 24) & 0xff;
-    gptr tbase = const_cast<gptr>(layer_base(a.tgt, kind, mx & 0xffff)) +
-                 static_cast<int64_t>((mx >> 16) - a.tgt.head_offset) * D * 2 + (hh * 32 + g * 8) * 2;
-    const CB_GLOBAL float* rcos = gtab(a.cos_tab) + tth * a.theta_stride;
-    const CB_GLOBAL float* rsin = gtab(a.sin_tab) + tth * a.theta_stride;
-
-    // The job's packed W [member][row tile][k-step][term][lane]: this wave's
-    // fragments of stage t (member k, k-step ks; stages are k-step pairs
-    // {q, q + 2} of each member, q = 0 then 1) for row tiles
-    // (rl >> 1) * 4 + hh * 2 + (rl & 1).
-    gcptr wjob = as_global(a.w + static_cast<size_t>(it.job) * Sup * Gm<128, uint16_t>::W_U4) + lane * 16;
-    auto issue_w = [&](int t, uint4 (&dst)[4][2]) __attribute__((always_inline)) {
-      const int p = t >> 1, q = p >= Sup ? 1 : 0, k = p - q * Sup, ks = q + 2 * (t & 1);
 #pragma unroll
-      for (int rl = 0; rl < 4; ++rl) {
-        const int rt = (rl >> 1) * 4 + hh * 2 + (rl & 1);
+    for (int vh = 0; vh < 2; ++vh) {
+      // Run v = 2vh, 2vh + 1: dims 32tt + 16vh + 8h + 0..7 (16 bytes).
+      uint32_t o1[4], o2[4];
 #pragma unroll
-        for (int tm = 0; tm < 2; ++tm)
-          dst[rl][tm] = gload<uint4>(wjob + (((static_cast<int64_t>(k) * 8 + rt) * 4 + ks) * 2 + tm) * (kWave * 16));
+      for (int i2 = 0; i2 < 4; ++i2) {
+        o1[i2] = pack_bf16(y1[8 * vh + 2 * i2], y1[8 * vh + 2 * i2 + 1]);
+        o2[i2] = pack_bf16(y2[8 * vh + 2 * i2], y2[8 * vh + 2 * i2 + 1]);
       }
-    };
-
-    auto run = [&](auto is_k_tag) {
-      constexpr bool IS_K = decltype(is_k_tag)::value;
-      constexpr int XT = IS_K ? 2 : 1;
-      f32x4 acc[4][8];  // [row tile p*2 + q'][column tile]
-      uint4 wr[2][4][2];  // W fragments of the current stage and the next
-      issue_w(0, wr[0]);
-      auto stage = [&](int t, const uint4 (&cur)[4][2], uint4 (&nxt)[4][2]) __attribute__((always_inline)) {
-        if (t + 1 < nstage) issue_w(t + 1, nxt);
-        const int slot = n % kSupRing;
-        sup_wait(S, &S.full[slot], 4 * (n / kSupRing + 1), a.err);
-        const SupStage& B = S.ring[slot];
-        if (t == 0) {
-          // Each row tile's bias is the accumulator input of its first
-          // product (the producers wrote it before the item's first stage).
-          // Set once per item here, so the products below carry no per-MFMA
-          // branch and no wait for the outstanding fragment reads.
-#pragma unroll
-          for (int rl = 0; rl < 4; ++rl) {
-            const float* bp = S.bias[parity] + (rl >> 1) * 64 + hh * 32 + g * 8 + (rl & 1) * 4;
-            const f32x4 b = f32x4{bp[0], bp[1], bp[2], bp[3]};
-#pragma unroll
-            for (int c = 0; c < 8; ++c) acc[rl][c] = b;
-          }
-        }
-        bf16x8 wv[4][2];
-#pragma unroll
-        for (int rl = 0; rl < 4; ++rl)
-#pragma unroll
-          for (int tm = 0; tm < 2; ++tm) wv[rl][tm] = __builtin_bit_cast(bf16x8, cur[rl][tm]);
-        // Input fragments flow through a three-slot ring, read two column
-        // tiles ahead of their products; the scheduling barrier keeps the
-        // compiler from sinking each read next to its first use.
-        bf16x8 xv[3][XT];
-        auto read_x = [&](int c, bf16x8 (&dst)[XT]) {
-#pragma unroll
-          for (int x = 0; x < XT; ++x) dst[x] = __builtin_bit_cast(bf16x8, B.x[8 * cb + c][x][lane]);
-        };
-        read_x(0, xv[0]);
-        read_x(1, xv[1]);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          if (c + 2 < 8) read_x(c + 2, xv[(c + 2) % 3]);
-          if (c == 7) {
-            // Every read of this stage is issued: release the buffer once they are done.
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) __hip_atomic_fetch_add(lds_u32(&S.empty[slot]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          }
-          for_products<XT, 2>([&](int ii, int jj) {
-#pragma unroll
-            for (int rl = 0; rl < 4; ++rl) acc[rl][c] = mfma(wv[rl][jj], xv[c % 3][ii], acc[rl][c]);
-          });
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        ++n;
-      };
-      // Two stages per step, so the W register slots are compile-time
-      // constants (a runtime-indexed register array would live in scratch).
-      for (int t = 0; t < nstage; t += 2) {
-        stage(t, wr[0], wr[1]);
-        stage(t + 1, wr[1], wr[0]);
-      }
-      // Epilogue: target RoPE, cast, store.
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int tok = (8 * cb + c) * 16 + col;
-        const int row = S.trow[parity][tok];
-        float y1[8], y2[8];
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            y1[4 * q + i] = acc[q][c][i];
-            y2[4 * q + i] = acc[2 + q][c][i];
-          }
-        if constexpr (IS_K) {
-          const int tp = S.tpos[parity][tok];
-          float cv[8], sv[8];
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int64_t off = tab_chunk<16>(tp, 2 * (g & 1) + u, 2 * hh + (g >> 1));
-            const float4 c4 = *reinterpret_cast<const CB_GLOBAL float4*>(rcos + off);
-            const float4 s4 = *reinterpret_cast<const CB_GLOBAL float4*>(rsin + off);
-            cv[4 * u] = c4.x; cv[4 * u + 1] = c4.y; cv[4 * u + 2] = c4.z; cv[4 * u + 3] = c4.w;
-            sv[4 * u] = s4.x; sv[4 * u + 1] = s4.y; sv[4 * u + 2] = s4.z; sv[4 * u + 3] = s4.w;
-          }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float a1 = y1[e], a2 = y2[e];
-            y1[e] = __builtin_fmaf(a1, cv[e], -(a2 * sv[e]));
-            y2[e] = __builtin_fmaf(a2, cv[e], a1 * sv[e]);
-          }
-        }
-        uint32_t o1[4], o2[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          o1[i] = pack_bf16(y1[2 * i], y1[2 * i + 1]);
-          o2[i] = pack_bf16(y2[2 * i], y2[2 * i + 1]);
-        }
-        gptr dst = row >= 0 ? tbase + static_cast<int64_t>(row) * a.tgt.row_stride_b : sink;
-        gstore<uint4>(dst, make_uint4(o1[0], o1[1], o1[2], o1[3]));
-        gstore<uint4>(dst + HALF * 2, make_uint4(o2[0], o2[1], o2[2], o2[3]));
-      }
-    };
-    if (kind == CB_KIND_K) run(std::integral_constant<bool, true>{});
-    else run(std::integral_constant<bool, false>{});
+      const int off = (32 * tt + 16 * vh + 8 * h) * 2;
+      gstore<uint4>(dst + off, make_uint4(o1[0], o1[1], o1[2], o1[3]));
+      gstore<uint4>(dst + off + 128, make_uint4(o2[0], o2[1], o2[2], o2[3]));
+    }
   }
 }
 
 __global__ __launch_bounds__(kSupThreads, 1) void map_install_support_kernel(MapArgs a) {
-  __shared__ SupShared S;
-  if (threadIdx.x < kSupRing) {
-    S.full[threadIdx.x] = 0;
-    S.empty[threadIdx.x] = 0;
-  }
-  if (threadIdx.x == 0) S.abort = 0;
-  __syncthreads();
+  __shared__ uint4 lds[4 * kSupStageU4];  // W ring: four 16 KB stage slots
+  __shared__ uint4 lds_xa[kSupWaves * 256];  // source rows of even pairs, 4 KB per wave
+  __shared__ uint4 lds_xb[kSupWaves * 256];  // and of odd pairs
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   SupItems items;
   items.x = blockIdx.x & 7;
   items.nwg = gridDim.x >> 3;
-  items.y = blockIdx.x >> 3;
-  items.next = items.y;
-  if (__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) < kSupRoleWaves) sup_consumer(a, S, items);
-  else sup_producer(a, S, items);
+  items.next = blockIdx.x >> 3;
+  uint32_t slot = 0;  // ring slot of the last stage run
+  int errbits = 0;
+  SupItems::Item it;
+  for (; items.get(a, it); items.next += items.nwg) {
+    SupLane I;
+    I.job = __builtin_amdgcn_readfirstlane(it.job);
+    const int* jm = reinterpret_cast<const int*>(a.jobs + I.job);
+    const int meta_y = cload(jm + 1), meta_z = cload(jm + 2);
+    I.kind = meta_y & 0xff;
+    I.lo = it.lo;
+    I.hi = it.hi;
+    const int sth = (meta_y >> 16) & 0xff;
+    const bool shared = (meta_z & kJobSharedTables) != 0;
+    I.ucos = gtab(shared ? a.cos_tab : a.ucos_tab) + sth * a.theta_stride;
+    I.usin = gtab(shared ? a.sin_tab : a.usin_tab) + sth * a.theta_stride;
+    const int n = it.hi - it.lo;
+    const int pt = 32 * wave + (lane & 31);
+    const int tk = it.lo + min(pt, n - 1);
+    I.live = pt < n;
+    const int64_t srow = row_of(a.src, tk);
+    const int64_t drow = row_of(a.tgt, tk);
+    const bool sok = srow >= 0 && srow < a.src.rows;
+    const bool dok = drow >= 0 && drow < a.tgt.rows;
+    if (I.live && lane < 32) errbits |= (sok ? 0 : 1) | (dok ? 0 : 2);
+    I.soff = I.live && sok ? srow * a.src.row_stride_b : -1;
+    // A token whose source row is out of range writes nothing.
+    I.trow = I.live && sok && dok ? static_cast<int32_t>(drow) : -1;
+    I.pos = position_of(a, tk);
+    if (I.kind == CB_KIND_K) support_item<true>(a, lds, lds_xa, lds_xb, I, wave, slot);
+    else support_item<false>(a, lds, lds_xa, lds_xb, I, wave, slot);
+  }
+  // The last item's trailing W and row requests (repeats of its last stage)
+  // write LDS: they land before the workgroup ends.
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  if (errbits) atomicOr(a.err, errbits);
 }
 
 // ---------------------------------------------------------------------------
@@ -1726,7 +1750,7 @@ __global__ __launch_bounds__(kThreads) void map_install_gen_kernel(MapArgs a) {
 
 // Pack fp32 W[orig][s*D][D] into bf16 split terms in MFMA A-fragment order,
 // and permute the bias to sorted job order.
-template <int D, int NTW, bool GROUP>
+template <int D, int NTW>
 __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __restrict__ bias,
                                     const int32_t* __restrict__ order, int njobs, int S,
                                     uint16_t* __restrict__ wp, float* __restrict__ bp) {
@@ -1741,7 +1765,7 @@ __global__ void pack_weights_kernel(const float* __restrict__ w, const float* __
     const int t = rem % NTW; rem /= NTW;
     const int ks = rem % KS; rem /= KS;
     const int rt = rem % RT; rem /= RT;
-    const int fo = GROUP ? grp_out_dim(rt, lane & 15) : gen_out_dim(D, rt, lane & 15);
+    const int fo = gen_out_dim(D, rt, lane & 15);
     const int k = rem % S; rem /= S;
     const int j = static_cast<int>(rem);
     const int src_job = order[j];
@@ -2404,15 +2428,15 @@ int to_dev_rows(const cb_rows& r, int elem_bytes, DevRows* out, int align = 16) 
   return CB_OK;
 }
 
-template <int D, int NTW, bool GROUP = false>
+template <int D, int NTW>
 void launch_pack(const cb_plan_desc* d, const int32_t* d_order, uint16_t* wp, float* bp) {
-  hipLaunchKernelGGL((pack_weights_kernel<D, NTW, GROUP>), dim3(1024), dim3(256), 0, 0, d->d_weight,
+  hipLaunchKernelGGL((pack_weights_kernel<D, NTW>), dim3(1024), dim3(256), 0, 0, d->d_weight,
                      d->d_bias, d_order, d->num_jobs, d->support, wp, bp);
 }
 
 template <typename SameGroup>
-int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup same_group,
-               cb_plan* p) {
+int plan_build(const cb_plan_desc* d, const std::vector<int>& order, const std::vector<int>& mperm,
+               SameGroup same_group, cb_plan* p) {
   const int D = d->head_dim, S = d->support, nj = d->num_jobs;
   int64_t bytes = 0;
   CB_HIP(hipGetDevice(&p->device));
@@ -2445,7 +2469,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
                             (d->job_target_theta[j] << 24),
                         0, j);
     for (int k = 0; k < S; ++k) {
-      const int sl = d->job_source_layer[j * S + k], sh = d->job_source_head[j * S + k];
+      const int m = mperm[static_cast<size_t>(j) * S + k];
+      const int sl = d->job_source_layer[j * S + m], sh = d->job_source_head[j * S + m];
       pairs[static_cast<size_t>(i) * S + k] = sl | (sh << 16);
       p->max_src_layer = std::max(p->max_src_layer, sl);
       p->min_src_head = std::min(p->min_src_head, sh);
@@ -2474,6 +2499,40 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   for (int c = 0; c < d->num_windows; ++c)
     if (p->cls_unit_begin[c] < 0) p->cls_unit_begin[c] = p->cls_unit_end[c] = 0;
   p->num_units = static_cast<int>(unit_job.size());
+  if (p->support_gemm) {
+    // The support kernel gives XCD x units x, x + 8, ... of each class. Place
+    // the units so that these are a contiguous run of the sorted keys jobs
+    // followed by one of the sorted values jobs (each XCD gets its share of
+    // both kinds, whose costs differ), so that jobs an XCD runs together
+    // share source layers. Units are single jobs here.
+    for (int c = 0; c < d->num_windows; ++c) {
+      const int cb = p->cls_unit_begin[c], n = p->cls_unit_end[c] - cb;
+      std::vector<int32_t> kj, vj;
+      for (int u = cb; u < cb + n; ++u) ((jobs[unit_job[u]].y & 0xff) == CB_KIND_K ? kj : vj).push_back(u);
+      std::vector<int32_t> perm(n);
+      bool ok = true;
+      int kpos = 0, vpos = 0;
+      for (int x = 0; x < 8 && ok; ++x) {
+        const int mine = n > x ? (n - x + 7) / 8 : 0;
+        const int nk = static_cast<int>(kj.size()) * (x + 1) / 8 - static_cast<int>(kj.size()) * x / 8;
+        const int nv = mine - nk;
+        if (nv < 0 || vpos + nv > static_cast<int>(vj.size())) ok = false;
+        for (int jl = 0; ok && jl < mine; ++jl) perm[x + 8 * jl] = jl < nk ? kj[kpos + jl] : vj[vpos + jl - nk];
+        kpos += nk;
+        vpos += std::max(nv, 0);
+      }
+      if (!ok) continue;  // leave the sorted order
+      std::vector<int32_t> uj(n), un(n), ug(n);
+      for (int i = 0; i < n; ++i) {
+        uj[i] = unit_job[perm[i]];
+        un[i] = unit_njobs[perm[i]];
+        ug[i] = unit_group[perm[i]];
+      }
+      std::copy(uj.begin(), uj.end(), unit_job.begin() + cb);
+      std::copy(un.begin(), un.end(), unit_njobs.begin() + cb);
+      std::copy(ug.begin(), ug.end(), unit_group.begin() + cb);
+    }
+  }
   {
     int cus = 0;
     CB_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device));
@@ -2548,8 +2607,11 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
   if ((rc = upload(&p->d_pool, nullptr, pool_bytes, &bytes))) return rc;
   CB_HIP(hipMemset(p->d_pool, 0, pool_bytes));
   int32_t* d_order = nullptr;
-  CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), order.size() * 4));
+  int32_t* d_mperm = nullptr;
+  CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), (order.size() + mperm.size()) * 4));
+  d_mperm = d_order + order.size();
   hipError_t e = hipMemcpy(d_order, order.data(), order.size() * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(d_mperm, mperm.data(), mperm.size() * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
     uint16_t* wp = static_cast<uint16_t*>(p->d_w);
     if (p->generic)
@@ -2560,7 +2622,8 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, SameGroup s
     else if (D == 64)
       launch_pack<64, 3>(d, d_order, wp, p->d_bias);
     else if (p->support_gemm)
-      launch_pack<128, 2, true>(d, d_order, wp, p->d_bias);
+      hipLaunchKernelGGL(pack_support_kernel, dim3(1024), dim3(256), 0, 0, d->d_weight, d->d_bias, d_order,
+                         d_mperm, d->num_jobs, d->support, wp, p->d_bias);
     else
       launch_pack<128, 2>(d, d_order, wp, p->d_bias);
     e = hipGetLastError();
@@ -3067,6 +3130,25 @@ int cb_plan_create(const cb_plan_desc* d, cb_plan** out) {
     }
   }
 
+  // Member order within a job: as given, except for the support kernel
+  // (bf16, head_dim 128, support > 1), which visits a job's source pairs in
+  // ascending (layer, head) order so that jobs sharing source layers visit
+  // them at about the same time (the sum over members is then taken in that
+  // order; its W rows are packed to match).
+  std::vector<int> mperm(static_cast<size_t>(nj) * S);
+  for (int j = 0; j < nj; ++j) {
+    int* m = mperm.data() + static_cast<size_t>(j) * S;
+    std::iota(m, m + S, 0);
+    if (S > 1 && D == 128 && d->io_dtype == CB_DTYPE_BF16)
+      std::stable_sort(m, m + S, [&](int u, int v) {
+        const int lu = d->job_source_layer[j * S + u], lv = d->job_source_layer[j * S + v];
+        if (lu != lv) return lu < lv;
+        return d->job_source_head[j * S + u] < d->job_source_head[j * S + v];
+      });
+  }
+  auto src_layer = [&](int j, int k) { return d->job_source_layer[j * S + mperm[static_cast<size_t>(j) * S + k]]; };
+  auto src_head = [&](int j, int k) { return d->job_source_head[j * S + mperm[static_cast<size_t>(j) * S + k]]; };
+
   // Sort jobs: window class, kind, RoPE theta sets, source pairs, then target
   // position. A group (same class, kind, thetas and source pairs) reads the
   // same source rows and tables.
@@ -3079,10 +3161,13 @@ int cb_plan_create(const cb_plan_desc* d, cb_plan** out) {
       return d->job_source_theta[x] < d->job_source_theta[y];
     if (d->job_target_theta[x] != d->job_target_theta[y])
       return d->job_target_theta[x] < d->job_target_theta[y];
+    // Support lists usually keep to one source head: jobs of a head sort
+    // together, in the order of their source layers (depth).
+    if (S > 1 && src_head(x, 0) != src_head(y, 0)) return src_head(x, 0) < src_head(y, 0);
     for (int k = 0; k < S; ++k) {
-      const int a0 = d->job_source_layer[x * S + k], b0 = d->job_source_layer[y * S + k];
+      const int a0 = src_layer(x, k), b0 = src_layer(y, k);
       if (a0 != b0) return a0 < b0;
-      const int a1 = d->job_source_head[x * S + k], b1 = d->job_source_head[y * S + k];
+      const int a1 = src_head(x, k), b1 = src_head(y, k);
       if (a1 != b1) return a1 < b1;
     }
     if (d->job_target_layer[x] != d->job_target_layer[y])
@@ -3096,14 +3181,12 @@ int cb_plan_create(const cb_plan_desc* d, cb_plan** out) {
         d->job_target_theta[x] != d->job_target_theta[y])
       return false;
     for (int k = 0; k < S; ++k)
-      if (d->job_source_layer[x * S + k] != d->job_source_layer[y * S + k] ||
-          d->job_source_head[x * S + k] != d->job_source_head[y * S + k])
-        return false;
+      if (src_layer(x, k) != src_layer(y, k) || src_head(x, k) != src_head(y, k)) return false;
     return true;
   };
 
   cb_plan* p = new cb_plan();
-  int rc = plan_build(d, order, same_group, p);
+  int rc = plan_build(d, order, mperm, same_group, p);
   // The plan's device is current here: look up its no-allocation workspace.
   if (rc == CB_OK) rc = scratch_setup(p->device);
   if (rc != CB_OK) {
