@@ -672,8 +672,8 @@ def support_bench(steps: int, warmup: int, cpu: bool = True) -> dict:
                                "head_dim 128, 4096 tokens, page 16"},
         "roofline": {"bound": "mfma", "achieved": main["algorithmic_tflops"], "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": main["algorithmic_frac"], "traffic": None,
-                     "kernel": "map_install_support_kernel (256-token items, producer/consumer waves "
-                               "over an LDS ring, split-bf16 MFMA)",
+                     "kernel": "map_install_support_kernel (256-token items, 32x32 split-bf16 MFMA, "
+                               "W and source rows staged by LDS DMA)",
                      "executed_frac": main["executed_frac"], "kernel_ms_mean": main["kernel_ms_mean"]},
         "legs": legs,
     }
