@@ -88,3 +88,29 @@ def test_random_batches_equal_per_request_installs(seed):
     h = synthetic.make_handoff(sh, target_pages=pages, fill_target="zeros")
     spans, bt = _batch(lengths, positions, prefixes, pages, seed=seed)
     check_batch_equals_single(h, spans, bt.to(h.target_pool.device))
+
+
+# Large supports through the support kernel (bf16, head_dim 128): window
+# classes holding fewer jobs than there are XCDs, an odd number of keys and
+# values jobs per class (the plan's per-XCD placement of keys and values
+# runs then takes its fallback on some classes), members that are not in
+# layer order (the kernel visits them sorted), and a partial last item.
+@pytest.mark.parametrize("ls,hs,lt,ht,support,windows,tokens,page", [
+    (16, 3, 7, 3, 8, [None, 300, None, 129, 300, None, 2], 700, 16),
+    (20, 1, 3, 1, 12, None, 520, 1),
+    (12, 2, 5, 2, 8, [300, None, 300, None, 129], 300, 16),
+])
+def test_large_supports_match_oracle(ls, hs, lt, ht, support, windows, tokens, page):
+    print(f"support {support}: {ls}x{hs} -> {lt}x{ht} T={tokens} page={page} windows={windows}", flush=True)
+    sh = synthetic.Shape(f"support{support}_{lt}x{ht}", ls, hs, lt, ht, 128, tokens, torch.bfloat16,
+                         list(range(ls)), source_theta=1e4, target_theta=[1e6] * lt, windows=windows,
+                         head_map="identity", page_size=page, seed=300 + support + lt, support=support)
+    h = synthetic.make_handoff(sh, fill_target=None)
+    g = torch.Generator(device="cuda").manual_seed(support + lt)
+    for data in (h.target_pool.k_data, h.target_pool.v_data):
+        data.copy_(torch.randn(data.shape, generator=g, device="cuda").to(data.dtype))
+    before = _cpu_pool(h.target_pool)
+    h.run()
+    assert h.mapper.plan.read_errors() == 0
+    mapped, tgt_slots = _oracle_install(h, before)
+    _check_pools(h, before, mapped, tgt_slots)
