@@ -1045,7 +1045,7 @@ __global__ __launch_bounds__(kStreamThreads) void map_install_stream_kernel(MapA
 //     and their RoPE partners) go into its own two-buffer LDS area two
 //     stages ahead, 16 tokens x one 64-byte sector per instruction.
 // Without these two distances the gathers' latency, not the MFMAs, set the
-// kernel's pace: the scattered 64-byte sectors of the token rows mostly come
+// kernel's pace: the token rows are scattered 64-byte sectors, many of them
 // from beyond L2.
 //
 // Every wave produces its own input: the split bf16 terms of the next k-step
@@ -2859,7 +2859,7 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
   int chunk = tokens_per_workgroup > 0 ? tokens_per_workgroup : default_tokens;
   if (tokens_per_workgroup < 0 || chunk < unit || chunk % unit)
     return fail(CB_EINVAL, "tokens_per_workgroup must be a positive multiple of %d", unit);
-  // The support kernel's items are fixed 128-token blocks; the knob does not apply.
+  // The support kernel's items are fixed 256-token blocks; the knob does not apply.
   if (p->support_gemm) chunk = kSupTile;
   a.w = static_cast<const uint4*>(p->d_w);
   a.bias = p->d_bias;
