@@ -465,36 +465,72 @@ def delta_state_bench(steps: int, warmup: int) -> dict:
 SPIN_CYCLES = 200_000_000  # GPU spin ahead of short timed launches (tens of ms)
 
 
-def delivery_bench(steps: int, warmup: int) -> dict:
-    """Receiver-side delivery of the TP4 share's selected source layers in
-    2048-token blocks (two slots), timed per block; and the whole block-wise
-    handoff (deliver, then map, per block, on one stream) against the fused
-    map from the pool."""
+def _delivered_handoff(tokens: int, steps: int, warmup: int, *, two_streams_only: bool = False) -> dict:
+    """Block-wise handoff of a TP4-share prefix of ``tokens`` through two
+    2048-token receiver slots: delivery then map per block on one stream, the
+    same with delivery on its own stream (a block's gather overlaps the map of
+    the block before it), and the fused map from the pool. Milliseconds per
+    handoff, device time of ``steps`` handoffs back to back."""
     import torch
 
     from cachebridge_amd import synthetic
     from cachebridge_amd.online.delivery import SelectedBlockDelivery, map_install_delivered
 
-    sh = synthetic.shape("tp4")
-    h = synthetic.make_handoff(sh)
+    sh = synthetic.shape("tp4", tokens=tokens)
+    h = synthetic.make_handoff(sh, target_pages=max(4096, 4 * ((tokens + 15) // 16)), device_source=True)
     block = 2048
-    d = SelectedBlockDelivery(h.source_pool, h.source_slots, layers=h.mapper.source_layers, block_tokens=block)
     compute = torch.cuda.current_stream()
     spans = [(a, min(a + block, sh.tokens)) for a in range(0, sh.tokens, block)]
+    out = {"tokens": tokens, "blocks": len(spans)}
 
-    def pipelined():
-        for i, (a, b) in enumerate(spans):
-            d.deliver(i % 2, a, b)
-            map_install_delivered(h.mapper, d, i % 2, h.target_pool, block_table=h.block_table, page_size=16,
-                                  prefix_length=sh.tokens, stream=compute)
+    def timed(fn) -> float:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(SPIN_CYCLES)  # the host enqueues while the GPU spins
+        e0.record(compute)
+        for _ in range(steps):
+            fn()
+        e1.record(compute)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
 
-    for _ in range(warmup):
-        pipelined()
-    torch.cuda.synchronize()
+    for label, stream in (("one_stream_ms", None), ("two_stream_ms", torch.cuda.Stream())):
+        d = SelectedBlockDelivery(h.source_pool, h.source_slots, layers=h.mapper.source_layers,
+                                  block_tokens=block, stream=stream)
+
+        def handoff():
+            if d.stream != compute:  # no delivery runs ahead of the timed region or the last handoff
+                d.stream.wait_stream(compute)
+            for i, (a, b) in enumerate(spans):
+                d.deliver(i % 2, a, b)
+                map_install_delivered(h.mapper, d, i % 2, h.target_pool, block_table=h.block_table,
+                                      page_size=16, prefix_length=sh.tokens, stream=compute)
+
+        out[label] = round(timed(handoff), 4)
+        out["delivery"] = d
+    out["fused_ms"] = round(timed(h.run), 4)
+    out["shape"] = sh
+    return out
+
+
+def delivery_bench(steps: int, warmup: int) -> dict:
+    """Receiver-side delivery of the TP4 share's selected source layers in
+    2048-token blocks (two slots), timed per block; and the whole block-wise
+    handoff (deliver, then map, per block, on one stream and with delivery on
+    a stream of its own) against the fused map from the pool, at 4096 and at
+    32768 tokens."""
+    import torch
+
+    short = _delivered_handoff(4096, steps, warmup)
+    d, sh = short.pop("delivery"), short.pop("shape")
+    block = 2048
     # Delivery kernel alone: `steps` blocks back to back on the delivery stream.
     # A block's gather (~20 us) is shorter than the host's deliver() call, so a
     # spin kernel first keeps the GPU busy while the host enqueues them; the
     # events then bracket GPU time only.
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(d.stream):
         torch.cuda._sleep(SPIN_CYCLES)
@@ -506,21 +542,8 @@ def delivery_bench(steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     deliver_ms = e0.elapsed_time(e1) / steps
     moved = 2 * 2 * len(d.layers) * block * sh.source_heads * sh.head_dim * 2  # read + write
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(SPIN_CYCLES)
-    e0.record(compute)
-    for _ in range(steps):
-        pipelined()
-    e1.record(compute)
-    torch.cuda.synchronize()
-    pipe_ms = e0.elapsed_time(e1) / steps
-    torch.cuda._sleep(SPIN_CYCLES)
-    e0.record(compute)
-    for _ in range(steps):
-        h.run()
-    e1.record(compute)
-    torch.cuda.synchronize()
-    fused_ms = e0.elapsed_time(e1) / steps
+    long = _delivered_handoff(32768, min(10, steps), min(warmup, 2))
+    long.pop("delivery"), long.pop("shape")
     gbs = moved / (deliver_ms * 1e-3) / 1e9
     return {
         "metric": "selected-layer block delivery (receiver slot fill) GB/s, TP4 share, 2048-token blocks",
@@ -533,7 +556,8 @@ def delivery_bench(steps: int, warmup: int) -> dict:
                      "bytes_per_block": moved, "kernel_ms_mean": round(deliver_ms, 5)},
         "delivered_bytes_per_handoff": 2 * len(d.layers) * sh.tokens * sh.source_heads * sh.head_dim * 2,
         "all_layer_bytes_per_handoff": 2 * sh.source_layers * sh.tokens * sh.source_heads * sh.head_dim * 2,
-        "delivered_handoff_ms": round(pipe_ms, 4), "fused_handoff_ms": round(fused_ms, 4),
+        "delivered_handoff_ms": short["one_stream_ms"], "fused_handoff_ms": short["fused_ms"],
+        "block_handoffs": [short, long],
     }
 
 
