@@ -759,6 +759,81 @@ def staged_bench(steps: int, warmup: int, layer_chunk: int = 8) -> dict:
     }
 
 
+def overlap_bench(steps: int, warmup: int, reps: int = 6) -> dict:
+    """Independent handoffs back to back: ``steps`` (at most 64) requests of one plan
+    (same source rows, six disjoint sets of target pages used in turn) on one
+    stream, and the same requests spread round-robin over two and three
+    streams with no events between them, so that one launch's last
+    workgroups and the next launch's start share the CUs. Device time per
+    handoff (events on the caller's stream, which waits for every stream at
+    the end), median of ``reps`` interleaved repetitions."""
+    import statistics
+
+    import torch
+
+    from cachebridge_amd import synthetic
+    from cachebridge_amd.online.blocks import map_install_block
+
+    cur = torch.cuda.current_stream()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    out = {}
+    for name in ("tp4", "full", "gemma"):
+        sh = synthetic.shape(name)
+        npages = (sh.tokens + sh.page_size - 1) // sh.page_size
+        h = synthetic.make_handoff(sh, target_pages=max(sh.target_pages, 6 * npages), device_source=True)
+        g = torch.Generator().manual_seed(77)
+        free = torch.randperm(h.target_pool.pages, generator=g)[: 6 * npages].to(h.block_table.device)
+        tables = [free[i * npages:(i + 1) * npages].to(h.block_table.dtype) for i in range(6)]
+
+        def run(ns: int) -> None:
+            ss = [cur] if ns == 1 else streams[:ns]
+            for i in range(steps):
+                map_install_block(h.mapper, h.source_pool, h.source_slots, h.target_pool, start=0,
+                                  stop=sh.tokens, block_table=tables[i % 6], page_size=sh.page_size,
+                                  prefix_length=sh.tokens, stream=ss[i % ns])
+
+        def timed(ns: int) -> float:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            torch.cuda._sleep(SPIN_CYCLES)  # the host enqueues while the GPU spins
+            e0.record(cur)
+            for st in streams[:ns] if ns > 1 else ():
+                st.wait_stream(cur)
+            run(ns)
+            for st in streams[:ns] if ns > 1 else ():
+                cur.wait_stream(st)
+            e1.record(cur)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / steps
+
+        # A plan rotates its launches over 64 work-pool counter pairs, so no
+        # more than that many may be in flight at once: synchronize per mode.
+        for ns in (1, 2, 3):
+            for _ in range(warmup):
+                run(ns)
+            torch.cuda.synchronize()
+        res = {1: [], 2: [], 3: []}
+        for _ in range(reps):
+            for ns in (1, 2, 3):
+                res[ns].append(timed(ns))
+        err = h.mapper.plan.read_errors()
+        if err != 0:
+            raise RuntimeError(f"{name}: kernel error flags {err:#x}")
+        out[name] = {f"streams_{ns}_us": round(statistics.median(v), 1) for ns, v in res.items()}
+        del h, tables, free
+        torch.cuda.empty_cache()
+    t1, t2 = out["tp4"]["streams_1_us"], out["tp4"]["streams_2_us"]
+    return {
+        "metric": "independent TP4-share handoffs back to back, two streams (us per handoff)",
+        "value": t2, "unit": "us", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": WORKLOADS["tp4"], "requests_in_turn": 6, "repetitions": reps},
+        "roofline": None,
+        "one_stream_us": t1, "two_streams_over_one": round(t2 / t1, 3),
+        "workloads": out,
+    }
+
+
 def artifacts_bench(layers: int = 64, heads: int = 8, dim: int = 128, support: int = 8) -> dict:
     """Verified mapper load at the shipped recipe's geometry (64 target layers,
     8 KV heads, head_dim 128, 8 selected source layers: 512 MiB of fp32 maps)
@@ -855,6 +930,8 @@ def main() -> int:
                     help="only time the recurrent-state transform (Qwen3.5-style hybrid model)")
     ap.add_argument("--support", type=int, default=1, choices=(1, 8),
                     help="8: only time the support-8 maps at the TP4 share and the whole model")
+    ap.add_argument("--overlap", action="store_true",
+                    help="only time independent handoffs back to back on one, two and three streams")
     ap.add_argument("--staged", action="store_true",
                     help="only time the two-stream staged handoff against the fused launch")
     ap.add_argument("--layer-chunk", type=int, default=8, help="target layers per staged chunk")
@@ -873,6 +950,9 @@ def main() -> int:
         return 0
     if args.delivery:
         print(json.dumps(delivery_bench(args.steps, args.warmup)), flush=True)
+        return 0
+    if args.overlap:
+        print(json.dumps(overlap_bench(min(args.steps, 20), min(args.warmup, 3))), flush=True)
         return 0
     if args.cohort:
         print(json.dumps(cohort_bench(args.steps, args.warmup)), flush=True)
