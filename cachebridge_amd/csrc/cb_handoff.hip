@@ -2360,6 +2360,14 @@ struct cb_plan {
   uint32_t* d_pool = nullptr;
   mutable std::atomic<uint32_t> pool_seq{0};
   mutable std::atomic<uint32_t> capture_seq{0};
+  // Completion event and stream of the last pooled direct launch on each
+  // pair (created with the plan; guarded by split_mu). A pooled launch whose
+  // pair's previous pooled launch may still run on another stream makes its
+  // own stream wait for it, so launches in flight never share a pair: two
+  // that did would take chunk indices from one counter, and each would then
+  // write some of the other's chunks with its own request's rows.
+  hipEvent_t pair_done[kPoolSlots] = {};
+  mutable hipStream_t pair_stream[kPoolSlots] = {};
   // The last launch's split, for callers and tests (cb_plan_last_split).
   mutable std::atomic<int32_t> last_pool_chunks{0};
   mutable std::atomic<int32_t> last_workgroups{0};
@@ -2382,6 +2390,8 @@ void plan_free(cb_plan* p) {
                   p->d_pool};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
+  for (hipEvent_t e : p->pair_done)
+    if (e) (void)hipEventDestroy(e);
   delete p;
 }
 
@@ -2606,6 +2616,7 @@ int plan_build(const cb_plan_desc* d, const std::vector<int>& order, const std::
   const size_t pool_bytes = 2 * (kPoolSlots + kCapturePairs) * sizeof(uint32_t);
   if ((rc = upload(&p->d_pool, nullptr, pool_bytes, &bytes))) return rc;
   CB_HIP(hipMemset(p->d_pool, 0, pool_bytes));
+  for (hipEvent_t& e : p->pair_done) CB_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   int32_t* d_order = nullptr;
   int32_t* d_mperm = nullptr;
   CB_HIP(hipMalloc(reinterpret_cast<void**>(&d_order), (order.size() + mperm.size()) * 4));
@@ -2901,6 +2912,9 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
   a.total_items = static_cast<int32_t>(items);
   a.padded_items = static_cast<int32_t>((items + 7) / 8 * 8);
   int64_t grid_blocks = a.padded_items;
+  // Held from the cost-line split through the launch and its pair event.
+  std::unique_lock<std::mutex> held;
+  int tracked_pair = -1;
   if (ws) {
     int64_t unit_tokens = 0, subtiles = 0;
     for (int c = 0; c < p->num_windows; ++c) {
@@ -2934,7 +2948,7 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
     std::vector<int32_t> key{a.num_blocks, p->num_windows, allow_pool ? 1 : 0};
     for (int c = 0; c < p->num_windows; ++c) key.push_back(a.cls_subtiles[c]);
     const size_t nbk = static_cast<size_t>(a.num_blocks) + 1;
-    std::lock_guard<std::mutex> lock(p->split_mu);
+    held = std::unique_lock<std::mutex>(p->split_mu);
     if (key == p->split_key) {
       std::copy(p->split_unit.begin(), p->split_unit.end(), a.blk_unit);
       std::copy(p->split_sub.begin(), p->split_sub.end(), a.blk_sub);
@@ -2956,6 +2970,16 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
     const uint32_t pair = captured ? (allow_pool ? static_cast<uint32_t>(kPoolSlots) + capture_pair : 0u)
                                    : p->pool_seq.fetch_add(1, std::memory_order_relaxed) % kPoolSlots;
     a.pool_ctr = p->d_pool + 2 * static_cast<size_t>(pair);
+    if (!captured && a.pool_n > 0) {
+      // The pair's previous pooled launch ran on this stream (finished
+      // before this one starts) or is waited for unless it has finished.
+      if (p->pair_stream[pair] != s) {
+        const hipError_t q = hipEventQuery(p->pair_done[pair]);
+        if (q == hipErrorNotReady) CB_HIP(hipStreamWaitEvent(s, p->pair_done[pair], 0));
+        else if (q != hipSuccess) return fail(CB_EHIP, "hipEventQuery: %s", hipGetErrorString(q));
+      }
+      tracked_pair = static_cast<int>(pair);
+    }
   }
   p->last_pool_chunks.store(ws ? a.pool_n : 0, std::memory_order_relaxed);
   p->last_workgroups.store(static_cast<int32_t>(grid_blocks), std::memory_order_relaxed);
@@ -2971,6 +2995,11 @@ int launch_map(const cb_plan* p, MapArgs& a, const int64_t* first, const int64_t
     } else {
       if (pv) hipLaunchKernelGGL((map_install_stream_kernel<64, float, true>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((map_install_stream_kernel<64, float, false>), grid, block, 0, s, a);
+    }
+    if (tracked_pair >= 0) {
+      CB_HIP(hipGetLastError());
+      CB_HIP(hipEventRecord(p->pair_done[tracked_pair], s));
+      p->pair_stream[tracked_pair] = s;
     }
   } else if (p->generic) {
     const dim3 g(static_cast<unsigned>(grid_blocks)), b(kAnyThreads);

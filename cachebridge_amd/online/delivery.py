@@ -19,8 +19,8 @@ needs no cross-stream event. A separate stream (``stream=``) works, with event
 waits on both sides, but on one MI355X (ROCm 7.2) it is slower: a kernel
 waiting on another stream's event starts 10-12 us after the kernel before it
 on its own stream ends (about 1 us without the wait), and a gather running
-beside the map slows both (TP4 share, 2048-token blocks: map 67 -> 96 us,
-gather 20 -> 62 us), so 16 blocks take 1.73 ms instead of 1.45 ms.
+beside the map slows both (TP4 share, 2048-token blocks: map 69 -> 96 us,
+gather 20 -> 65 us), so 16 blocks take 1.76 ms instead of 1.47 ms.
 
 The mapper then reads a slot through a per-layer pointer table in which every
 delivered source layer points at its plane of the slot, so the plan and its

@@ -280,12 +280,14 @@ int cb_delta_state_transform(int32_t dtype, int64_t batch, int32_t k, int32_t v,
    from launches that overlap are merged. Synchronizes `stream`.
 
    Work-pool counters: direct launches of one plan rotate over 64 counter
-   pairs, so up to 64 of them may be in flight at once on any streams; a
-   launch recorded into a HIP graph takes a pair of its own (64 per plan;
-   later captured launches run without the pool), so graph replays never
-   share a pair with direct launches. Two replays of one graph that overlap
-   in time do share their pair, and more than 64 direct launches in flight
-   share pairs: such launches set bit 3. */
+   pairs. A launch that uses the pool and whose pair's previous such launch
+   ran on another stream makes its stream wait for that launch (an event
+   recorded with it) unless it has finished, so any number of direct launches
+   may be queued on any streams and none shares its pair. A launch recorded
+   into a HIP graph takes a pair of its own (64 per plan; later captured
+   launches run without the pool), so graph replays never share a pair with
+   direct launches. Two replays of one graph that overlap in time do share
+   their pair: they set bit 3. */
 int cb_plan_read_errors(cb_plan* plan, int32_t* flags, void* stream);
 
 #ifdef __cplusplus
