@@ -428,8 +428,9 @@ class HandoffPlan:
         """Synchronize ``stream`` and return/clear the device error flags.
 
         Bit 0: a source row out of range; bit 1: a target row out of range;
-        bit 2: a kernel's internal schedule failed; bit 3: a streaming launch
-        shared its work-pool counter pair with another launch in flight.
+        bit 2: a work-pool claim fell past the pool (a host-side
+        inconsistency); bit 3: a streaming launch shared its work-pool counter
+        pair with another launch in flight (overlapping replays of one graph).
         """
         flags = ctypes.c_int32(0)
         _lib.check(self.lib.cb_plan_read_errors(self._handle, ctypes.byref(flags),

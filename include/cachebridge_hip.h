@@ -272,12 +272,11 @@ int cb_delta_state_transform(int32_t dtype, int64_t batch, int32_t k, int32_t v,
                              void* d_out, int64_t out_stride, void* stream);
 
 /* Read and clear the plan's device error word (bit 0: source row out of
-   range, bit 1: target row out of range, bit 2: a kernel's internal schedule
-   failed -- a bounded wait of the support kernel timed out, or a work-pool
-   claim of the streaming kernel fell past its pool; bit 3: a streaming
-   launch found its work-pool counter pair shared with another launch of the
-   plan in flight, so rows may be missing). The word is one per plan: bits
-   from launches that overlap are merged. Synchronizes `stream`.
+   range, bit 1: target row out of range, bit 2: a work-pool claim of the
+   streaming kernel fell past its pool, a host-side inconsistency; bit 3: a
+   streaming launch found its work-pool counter pair shared with another
+   launch of the plan in flight, so rows may be missing). The word is one per
+   plan: bits from launches that overlap are merged. Synchronizes `stream`.
 
    Work-pool counters: direct launches of one plan rotate over 64 counter
    pairs. A launch that uses the pool and whose pair's previous such launch
