@@ -38,6 +38,7 @@ from dataclasses import dataclass, field
 
 import torch
 
+from .layouts import head_assignment
 from .mapper import HeadwiseMapper
 from .pool import PagedKVPool
 
@@ -120,8 +121,9 @@ def mapper_spec(sh: Shape) -> dict:
         selected = sorted(torch.randperm(sh.source_layers, generator=g)[:4].tolist())
     pick = torch.randint(0, len(selected), (lt, ht, 1), generator=g)
     layer = torch.tensor(selected, dtype=torch.int64)[pick]
-    if sh.head_map == "half":
-        head = (torch.arange(ht) // 2).view(1, ht, 1).expand(lt, ht, 1).clone()
+    if sh.head_map == "half":  # Gemma-style: target head h reads source head h // 2
+        heads = head_assignment(sh.source_heads, ht, [h // 2 for h in range(ht)])
+        head = torch.tensor(heads, dtype=torch.int64).view(1, ht, 1).expand(lt, ht, 1).clone()
     else:
         head = torch.randint(0, sh.source_heads, (lt, ht, 1), generator=g)
     std = 1.0 / math.sqrt(d)
@@ -155,7 +157,8 @@ def _support_spec(sh: Shape, g: torch.Generator) -> dict:
     std = 1.0 / math.sqrt(s * d)
     return {
         "assign_layer": layers[:, None, :].expand(lt, ht, s).clone(),
-        "assign_head": torch.arange(ht).view(1, ht, 1).expand(lt, ht, s).clone(),
+        "assign_head": torch.tensor(head_assignment(sh.source_heads, ht), dtype=torch.int64)
+        .view(1, ht, 1).expand(lt, ht, s).clone(),
         "k_weight": torch.randn(lt, ht, s * d, d, generator=g) * std,
         "v_weight": torch.randn(lt, ht, s * d, d, generator=g) * std,
         "k_bias": torch.randn(lt, ht, d, generator=g) * 0.1,
