@@ -157,7 +157,7 @@ def _support_spec(sh: Shape, g: torch.Generator) -> dict:
     std = 1.0 / math.sqrt(s * d)
     return {
         "assign_layer": layers[:, None, :].expand(lt, ht, s).clone(),
-        "assign_head": torch.tensor(head_assignment(sh.source_heads, ht), dtype=torch.int64)
+        "assign_head": torch.tensor(head_assignment(sh.source_heads, ht, list(range(ht))), dtype=torch.int64)
         .view(1, ht, 1).expand(lt, ht, s).clone(),
         "k_weight": torch.randn(lt, ht, s * d, d, generator=g) * std,
         "v_weight": torch.randn(lt, ht, s * d, d, generator=g) * std,
