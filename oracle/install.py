@@ -8,9 +8,12 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
   and ``cb/backends/sglang/runtime/r010_core.py:37-43``. SGLang v0.4.10.post2
   (commit 8cd344586e09669432d35c678b7cc208c0a6f47e) is an un-vendored
   dependency; its ``set_kv_buffer`` is restated as a plain row store
-  ``buffer[layer][loc] = k.to(dtype)``. PARITY UNPINNED against SGLang itself
-  (no reference test pins it); pinned here by invariants only: written rows
-  equal the mapped rows bit for bit and every other row is unchanged.
+  ``buffer[layer][loc] = k.to(dtype)``. SGLang's own code is not available
+  here. The restatement is pinned by the check the reference runs after its
+  installs through SGLang's pool (``rt/clean_adapter.py:638-652``: the rows at
+  ``indices`` of every layer bit-equal the written values) and by the
+  row-store invariant that every other row is unchanged
+  (``tests/test_oracle.py``).
 - ``pack_source_block`` / ``map_write_block``: ``cb/online/blocks.py:47-111``.
   Pinned by ``tests/test_blocks.py:33-65`` of the reference (restated as a test).
 - ``virtual_source_page``: re-index a source pool into a page whose layer

@@ -252,7 +252,11 @@ def test_row_store_writes_exactly_its_inputs_at_loc(dtype):
     ``loc`` of the named layer become exactly the given K and V rows (cast to
     the pool dtype when they arrive in another), every other row of that layer
     and every row of every other layer keep their bits, for int64 and int32
-    ``loc`` in any order."""
+    ``loc`` in any order. The first property is the one the reference asserts
+    after its own installs through SGLang's pool
+    (``rt/clean_adapter.py:638-652``: ``_get_key_buffer(layer)[indices]`` and
+    ``_get_value_buffer(layer)[indices]`` bit-equal the written values, layer
+    by layer, ``rt/`` = ``src/cachebridge/backends/sglang/runtime/``)."""
     g = torch.Generator().manual_seed(31)
     layers, rows, heads, dim = 3, 40, 2, 8
     fill = torch.randn(2, layers, rows, heads, dim, generator=g).to(dtype)
