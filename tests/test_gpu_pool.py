@@ -191,3 +191,61 @@ def test_pool_launches_64_apart_on_two_streams_install_both_requests():
         assert h.mapper.plan.read_errors() == 0, f"trial {trial}"
         assert torch.equal(fs.snapshot(pool, slots[0]), ref[0]), f"trial {trial}: request A"
         assert torch.equal(fs.snapshot(pool, slots[1]), ref[1]), f"trial {trial}: request B"
+
+
+def test_pool_launches_from_two_host_threads_install_both_requests():
+    """Two host threads launch one plan concurrently, each 40 pooled launches
+    (the TP4 share capped to 32 workgroups) of its own request on its own
+    stream, so that launches 64 apart in the plan's rotation come from
+    different threads and streams. Every launch must have its counter pair to
+    itself: both requests' rows equal those of launches run one at a time, and
+    no error bit is set."""
+    import threading
+
+    sh = synthetic.shape("tp4")
+    n = sh.tokens
+    npages = (n + sh.page_size - 1) // sh.page_size
+    print(f"two host threads, one plan: {sh.target_layers}x{sh.target_heads}, {n} tokens each, "
+          f"32 workgroups, 40 launches per thread", flush=True)
+    h = synthetic.make_handoff(sh, target_pages=3 * npages, device_source=True)
+    pool = h.target_pool
+    dev = pool.k_data.device
+    g = torch.Generator().manual_seed(13)
+    pages = torch.randperm(pool.pages, generator=g)[: 2 * npages].to(torch.int32)
+    tables = [pages[i * npages:(i + 1) * npages].to(dev) for i in range(2)]
+    slots = [synthetic.slots_from_pages(t.cpu(), n, sh.page_size).to(dev) for t in tables]
+
+    def run(i, stream=None):
+        map_install_block(h.mapper, h.source_pool, h.source_slots, pool, start=0, stop=n,
+                          block_table=tables[i], page_size=sh.page_size, prefix_length=n,
+                          stream=stream, tokens_per_workgroup=16384)
+
+    fs.fill_sentinel(pool)
+    run(0)
+    run(1)
+    assert h.mapper.plan.last_split()[0] > 0
+    assert h.mapper.plan.read_errors() == 0
+    ref = [fs.snapshot(pool, slots[0]), fs.snapshot(pool, slots[1])]
+    fs.fill_sentinel(pool)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(i):
+        try:
+            with torch.cuda.device(dev):
+                for _ in range(40):
+                    run(i, streams[i])
+        except Exception as exc:  # noqa: BLE001 -- reported by the main thread
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    assert h.mapper.plan.read_errors() == 0
+    assert torch.equal(fs.snapshot(pool, slots[0]), ref[0])
+    assert torch.equal(fs.snapshot(pool, slots[1]), ref[1])
